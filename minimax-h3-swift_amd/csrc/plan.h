@@ -1,0 +1,25 @@
+// The opaque plan behind h3hip_plan: tile lists (host and device), launch
+// order and decline policy. Immutable after h3hip_plan_create.
+#pragma once
+
+#include <cstdint>
+#include <vector>
+
+#include "../../include/ch3hip.h"
+
+struct h3hip_plan_s {
+  int32_t seq_len = 0;
+  int32_t seq_pad = 0;
+  int32_t n_tiles = 0;
+  int32_t heads = 0;
+  int32_t prefix_len = 0;
+  int32_t kind = 0;
+  int64_t nnz = 0;
+  h3hip_policy policy{};
+  std::vector<int32_t> row_ptr;  // host copy [n_tiles + 1]
+  std::vector<int32_t> col_idx;  // host copy [nnz]
+  std::vector<int32_t> work;     // launch order: (head << 16 | q_tile) or -1
+  int32_t* d_row_ptr = nullptr;
+  int32_t* d_col_idx = nullptr;
+  int32_t* d_work = nullptr;
+};

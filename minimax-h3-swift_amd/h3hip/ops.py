@@ -1,0 +1,175 @@
+"""Torch-facing calls into libch3hip.
+
+torch supplies device memory and the current HIP stream; every computation is
+one of the library's HIP kernels. Inputs must already be on the GPU: there is
+no host or torch fallback, and a declined call returns ``None`` so the caller
+can run its own dense path, exactly as the reference's backends decline.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from . import _lib as L
+from .topology import TilePlan
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _require_gpu_bf16(name: str, t: torch.Tensor):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (no host fallback exists)")
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+
+
+# ------------------------------------------------------------------ host tables
+
+def rope_pairs_axes(theta: float = 10000.0, dims=(32, 48, 48)):
+    """Per-pair (axis, inv_freq) for three-axis RoPE with the given channel split."""
+    n = sum(dims) // 2
+    ax = np.zeros(n, dtype=np.int32)
+    inv = np.zeros(n, dtype=np.float32)
+    got = L.lib().h3hip_rope_pairs_axes(theta, dims[0], dims[1], dims[2],
+                                        ax.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                        inv.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    L.check(min(got, 0))
+    return ax, inv
+
+
+def rope_pairs_h3(inv_freq: np.ndarray):
+    """H3RoPE's pair table from the checkpoint's inv_freq (H3Transformer.swift:64-78)."""
+    f = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    ax = np.zeros(3 * len(f), dtype=np.int32)
+    inv = np.zeros(3 * len(f), dtype=np.float32)
+    got = L.lib().h3hip_rope_pairs_h3(f.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(f),
+                                      ax.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                      inv.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    L.check(min(got, 0))
+    return ax, inv
+
+
+def positions_grid(prefix_len: int, frames: int, height: int, width: int) -> np.ndarray:
+    pos = np.zeros((prefix_len + frames * height * width, 3), dtype=np.float32)
+    got = L.lib().h3hip_positions_grid(prefix_len, frames, height, width,
+                                       pos.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    L.check(min(got, 0))
+    return pos
+
+
+def positions_packed(text_tokens: int, audio_t: int, latent_t: int, latent_h: int,
+                     latent_w: int, patch: int = 2) -> np.ndarray:
+    n = text_tokens + 2 * audio_t + latent_t * (latent_h // patch) * (latent_w // patch)
+    pos = np.zeros((n, 3), dtype=np.float64)
+    got = L.lib().h3hip_positions_packed(text_tokens, audio_t, latent_t, latent_h, latent_w,
+                                         patch,
+                                         pos.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    L.check(min(got, 0))
+    return pos
+
+
+# --------------------------------------------------------------------- prologue
+
+def qk_norm_rope(q_in: torch.Tensor, k_in: torch.Tensor, q_gamma: torch.Tensor,
+                 k_gamma: torch.Tensor, pos: torch.Tensor, pair_axis: torch.Tensor,
+                 pair_inv: torch.Tensor, *, heads: int, head_dim: int = 128,
+                 eps: float = 1e-6, rot: int | None = None, seq_pad: int | None = None,
+                 v_in: torch.Tensor | None = None, rounding: int = L.ROUND_REFERENCE,
+                 out=None):
+    """Fused RMSNorm + RoPE + head-major relayout of token-major Q and K.
+
+    q_in/k_in: [S, >= heads*head_dim] bf16 views sharing one row stride (e.g.
+    slices of a fused qkv projection). Returns (q_out, k_out, v_out) as
+    [heads, seq_pad, head_dim] bf16, or None when the geometry is declined."""
+    for name, t in (("q_in", q_in), ("k_in", k_in), ("q_gamma", q_gamma),
+                    ("k_gamma", k_gamma)):
+        _require_gpu_bf16(name, t)
+    if q_in.dim() != 2 or q_in.stride(1) != 1 or k_in.stride() != q_in.stride():
+        raise ValueError("q_in and k_in must be row-major 2-D views with the same row stride")
+    S = q_in.shape[0]
+    seq_pad = seq_pad or ((S + L.TILE - 1) // L.TILE) * L.TILE
+    rot = rot if rot is not None else 2 * pair_axis.numel()
+    if v_in is not None:
+        _require_gpu_bf16("v_in", v_in)
+        if v_in.stride() != q_in.stride():
+            raise ValueError("v_in must share q_in's row stride")
+    for name, t, dt in (("pos", pos, torch.float32), ("pair_axis", pair_axis, torch.int32),
+                        ("pair_inv", pair_inv, torch.float32)):
+        if not t.is_cuda or t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {dt} GPU tensor")
+    if pos.dim() != 2 or pos.shape[0] < S or pos.shape[1] != 3:
+        raise ValueError(f"pos must be [>= {S}, 3]")
+    if pair_axis.numel() < rot // 2 or pair_inv.numel() < rot // 2:
+        raise ValueError(f"pair tables must hold rot/2 = {rot // 2} entries")
+    if q_in.shape[1] < heads * head_dim or seq_pad % 4 or seq_pad < S:
+        raise ValueError("q_in narrower than heads*head_dim, or bad seq_pad")
+    if out is None:
+        dev = q_in.device
+        shape = (heads, seq_pad, head_dim)
+        q_out = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+        k_out = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+        v_out = torch.empty(shape, dtype=torch.bfloat16, device=dev) if v_in is not None else None
+    else:
+        q_out, k_out, v_out = out
+        for t in (q_out, k_out) + ((v_out,) if v_in is not None else ()):
+            if t.shape != (heads, seq_pad, head_dim) or not t.is_contiguous():
+                raise ValueError("outputs must be contiguous [heads, seq_pad, head_dim]")
+    rc = L.lib().h3hip_qk_norm_rope(_ptr(q_in), _ptr(k_in), q_in.stride(0), _ptr(v_in),
+                                    _ptr(q_gamma), _ptr(k_gamma), eps, _ptr(pos),
+                                    _ptr(pair_axis), _ptr(pair_inv), rot, rounding, S, seq_pad,
+                                    heads, head_dim, _ptr(q_out), _ptr(k_out), _ptr(v_out),
+                                    _stream(q_in))
+    if L.check(rc, allow_declined=True) == L.DECLINED:
+        return None
+    return q_out, k_out, v_out
+
+
+# -------------------------------------------------------------------- attention
+
+def bsattn_fwd(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+               scale: float | None = None, out_layout: int = L.OUT_HEAD_MAJOR,
+               out: torch.Tensor | None = None):
+    """Block-sparse attention over the plan's tiles; q/k/v [H, seq_pad, D] bf16.
+
+    Returns the output tensor, or None when the call is declined."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require_gpu_bf16(name, t)
+        if not t.is_contiguous() or t.dim() != 3 or t.shape[1] != plan.seq_pad:
+            raise ValueError(f"{name} must be contiguous [heads, {plan.seq_pad}, head_dim]")
+    H, _, D = q.shape
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    if out is None:
+        shape = (H, plan.seq_pad, D) if out_layout == L.OUT_HEAD_MAJOR else (plan.seq_pad, H * D)
+        out = torch.empty(shape, dtype=torch.bfloat16, device=q.device)
+    rc = L.lib().h3hip_bsattn_fwd(plan.handle, _ptr(q), _ptr(k), _ptr(v), H, D, scale,
+                                  _ptr(out), out_layout, _stream(q))
+    if L.check(rc, allow_declined=True) == L.DECLINED:
+        return None
+    return out
+
+
+def attend(plan: TilePlan, context, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+           scale: float, out: torch.Tensor | None = None):
+    """h3hip_attend: policy + geometry checks, then the sparse kernel.
+
+    ``context`` is an AttentionContext (or None, which declines)."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require_gpu_bf16(name, t)
+    H, _, D = q.shape
+    if out is None:
+        out = torch.empty((H, plan.seq_pad, D), dtype=torch.bfloat16, device=q.device)
+    cctx = None if context is None else ctypes.byref(context.to_c())
+    rc = L.lib().h3hip_attend(plan.handle, cctx, _ptr(q), _ptr(k), _ptr(v), H, D, scale,
+                              _ptr(out), _stream(q))
+    if L.check(rc, allow_declined=True) == L.DECLINED:
+        return None
+    return out

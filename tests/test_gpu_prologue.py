@@ -1,0 +1,153 @@
+"""The fused Q/K RMSNorm + RoPE + head-major prologue on the GPU vs the oracle.
+
+Gate of QKFusionTests.qkNormRoPECeiling (QKFusionTests.swift:64-110): worst
+relative RMS < 1e-3 and worst scaled ulp |d| / (|a| + rms) / 2^-7 < 8. With
+the reference rounding points the kernel is expected to be bit-identical to
+the oracle almost everywhere; the test requires >= 99.9% identical words.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _gpu import bits, note, to_gpu_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def gate(got_bits, want_bits):
+    import oracle as O
+    a = O.bf16_to_f32(want_bits).astype(np.float64)
+    b = O.bf16_to_f32(got_bits).astype(np.float64)
+    rms = np.sqrt(np.mean(a * a))
+    rel = np.sqrt(np.mean((a - b) ** 2)) / rms
+    ulp = np.max(np.abs(a - b) / (np.abs(a) + rms)) / 0.0078125
+    same = np.mean(got_bits == want_bits)
+    return rel, ulp, same
+
+
+def run_case(h3, orc, S, H, rot, rounding, fused_qkv=False, with_v=False, seed=3, h3_tables=False):
+    from h3hip import ops
+    D = 128
+    S_pad = (S + 127) // 128 * 128
+    inner = H * D
+    ld = 3 * inner if fused_qkv else inner
+    qkv = orc.randn_bf16((S, ld), seed)
+    if fused_qkv:
+        q_bits, k_bits, v_bits = qkv, qkv[:, inner:], qkv[:, 2 * inner:]
+    else:
+        q_bits = qkv
+        k_bits = orc.randn_bf16((S, ld), seed + 10)
+        v_bits = orc.randn_bf16((S, ld), seed + 20)
+    qg = orc.uniform_bf16((D,), seed + 1, 0.9, 1.1)
+    kg = orc.uniform_bf16((D,), seed + 2, 0.9, 1.1)
+    frames, hh, ww = 3, 8, 9
+    prefix = S - frames * hh * ww
+    assert prefix >= 0
+    pos = orc.positions_grid(prefix, frames, hh, ww)
+    if h3_tables:
+        axis, inv = ops.rope_pairs_h3((1.0 / 10000.0 ** (np.arange(16) / 16)).astype(np.float32))
+    else:
+        axis, inv = ops.rope_pairs_axes(10000.0, (32, 48, 48))
+    axis, inv = axis[:rot // 2], inv[:rot // 2]
+
+    g_qkv = to_gpu_bf16(qkv)
+    if fused_qkv:
+        gq, gk, gv = g_qkv[:, :inner], g_qkv[:, inner:2 * inner], g_qkv[:, 2 * inner:]
+    else:
+        gq, gk, gv = g_qkv, to_gpu_bf16(k_bits), to_gpu_bf16(v_bits)
+    note(f"prologue S={S} H={H} rot={rot} rounding={rounding} fused={fused_qkv} v={with_v}")
+    res = ops.qk_norm_rope(gq, gk, to_gpu_bf16(qg), to_gpu_bf16(kg),
+                           torch.from_numpy(pos).cuda(), torch.from_numpy(axis).cuda(),
+                           torch.from_numpy(inv).cuda(), heads=H, eps=1e-6, rot=rot,
+                           v_in=gv if with_v else None, rounding=rounding)
+    torch.cuda.synchronize()
+    q_out, k_out, v_out = res
+    qc, kc = np.ascontiguousarray(q_bits), np.ascontiguousarray(k_bits)
+    want_q = orc.qk_norm_rope(qc, qc.shape[1], S, S_pad, H, D, qg, 1e-6, pos, axis, inv, rot,
+                              rounding)
+    want_k = orc.qk_norm_rope(kc, kc.shape[1], S, S_pad, H, D, kg, 1e-6, pos, axis, inv, rot,
+                              rounding)
+    out = dict(q=(bits(q_out), want_q), k=(bits(k_out), want_k))
+    if with_v:
+        vv = np.ascontiguousarray(v_bits)[:, :inner].reshape(S, H, D).transpose(1, 0, 2)
+        want_v = np.zeros((H, S_pad, D), dtype=np.uint16)
+        want_v[:, :S] = vv
+        out["v"] = (bits(v_out), want_v)
+    return out
+
+
+@pytest.mark.parametrize("S,H,rot,rounding,h3t", [
+    (300, 3, 128, 0, False),     # ragged S, reference rounding, 32/48/48 table
+    (300, 3, 128, 1, False),     # fp32 rounding
+    (256, 5, 96, 0, True),       # the H3 model's table: rot 96, channels 96..127 pass through
+    (1000, 40, 128, 0, False),   # benchmark head count
+])
+def test_prologue_matches_oracle(h3, orc, S, H, rot, rounding, h3t):
+    res = run_case(h3, orc, S, H, rot, rounding, h3_tables=h3t)
+    for name in ("q", "k"):
+        got, want = res[name]
+        rel, ulp, same = gate(got, want)
+        assert rel < 1e-3 and ulp < 8, (name, rel, ulp)
+        if rounding == 0:
+            assert same >= 0.999, (name, same)
+        assert np.all(got[:, S:] == 0)
+
+
+def test_fused_qkv_input_and_v_relayout(h3, orc):
+    res = run_case(h3, orc, 216 + 40, 4, 128, 0, fused_qkv=True, with_v=True)
+    for name in ("q", "k"):
+        rel, ulp, same = gate(*res[name])
+        assert rel < 1e-3 and ulp < 8 and same >= 0.999
+    got_v, want_v = res["v"]
+    assert np.array_equal(got_v, want_v)
+
+
+def test_cfg5_full_size_sampled(h3, orc):
+    """Config 5: hidden [32000 x 5120] projected to Q, K (bf16 weights, std
+    0.02) by a setup GEMM, then the prologue over the 31x24x42 grid with the
+    637 text+audio tokens at position 0. Checked on sampled token rows of every
+    head, plus zeroed padding and finite output everywhere."""
+    from h3hip import configs as C, ops
+    shape = C.CFG3
+    S, S_pad, H, D = shape.seq_len, shape.seq_pad, shape.heads, 128
+    inner = H * D
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    note("cfg5 setup gemm")
+    hidden = torch.randn((S_pad, 5120), generator=g, device="cuda").to(torch.bfloat16)
+    wq = (torch.randn((5120, inner), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    wk = (torch.randn((5120, inner), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    q_in = (hidden @ wq)[:S]
+    k_in = (hidden @ wk)[:S]
+    del hidden
+    qg = orc.uniform_bf16((D,), 11, 0.9, 1.1)
+    kg = orc.uniform_bf16((D,), 12, 0.9, 1.1)
+    pos = ops.positions_grid(shape.prefix_len, shape.frames, shape.height, shape.width)
+    axis, inv = ops.rope_pairs_axes(10000.0, (32, 48, 48))
+    note("cfg5 prologue")
+    q_out, k_out, _ = ops.qk_norm_rope(q_in, k_in, to_gpu_bf16(qg), to_gpu_bf16(kg),
+                                       torch.from_numpy(pos).cuda(), torch.from_numpy(axis).cuda(),
+                                       torch.from_numpy(inv).cuda(), heads=H, eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.isfinite(q_out.float()).all() and torch.isfinite(k_out.float()).all()
+    assert torch.all(q_out[:, S:] == 0) and torch.all(k_out[:, S:] == 0)
+    rng = np.random.default_rng(0)
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(630, 645), np.arange(S - 8, S),
+                                     rng.integers(0, S, 256)]))
+    for name, src, gam, out in (("q", q_in, qg, q_out), ("k", k_in, kg, k_out)):
+        x_rows = bits(src[torch.from_numpy(rows).cuda()])
+        want = orc.qk_norm_rope(x_rows, inner, len(rows), len(rows), H, D, gam, 1e-6,
+                                np.ascontiguousarray(pos[rows]), axis, inv, 128)
+        got = bits(out[:, torch.from_numpy(rows).cuda()])
+        rel, ulp, same = gate(got, want)
+        assert rel < 1e-3 and ulp < 8 and same >= 0.999, (name, rel, ulp, same)
+
+
+def test_declines_unsupported_geometry_on_device(h3, orc):
+    from h3hip import ops
+    x = torch.zeros((4, 2 * 64), dtype=torch.bfloat16, device="cuda")
+    w = torch.ones(64, dtype=torch.bfloat16, device="cuda")
+    pos = torch.zeros((4, 3), dtype=torch.float32, device="cuda")
+    ax = torch.zeros(32, dtype=torch.int32, device="cuda")
+    inv = torch.ones(32, dtype=torch.float32, device="cuda")
+    assert ops.qk_norm_rope(x, x, w, w, pos, ax, inv, heads=2, head_dim=64, rot=64) is None
