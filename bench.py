@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Headline benchmark: block-sparse attention TFLOP/s over active tiles (and
+the fraction of the bf16 MFMA peak) at the 1344x768x5s shape, plus ms/layer.
+
+One step = one DiT layer's hot path at config 3 (S = 31,885 -> 32,000,
+40 heads x 128, local-window mask, 7,854 active 128x128 tiles per head):
+  1. the fused prologue: Q/K RMSNorm + 3D RoPE + head-major relayout of Q, K
+     and V, read from a token-major fused qkv buffer;
+  2. block-sparse attention over the plan's tiles, written token-major
+     ([S, heads*128], what the out-projection consumes).
+The tile plan is built once per shape (timed separately, not per layer).
+Inputs are synthetic and already resident in HBM when the timed region starts.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-extras]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "minimax-h3-swift_amd"))
+
+METRIC = "block-sparse attn TFLOP/s (active tiles) + % MFMA peak at 31k tokens; ms/layer"
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA, spec sheet
+PEAK_HBM_GBPS = 8000.0        # MI355X HBM3E, spec sheet
+FLOP_PER_TILE_HEAD = 4 * 128 ** 3   # QK^T and PV over one 128x128 tile, head_dim 128
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(shape, plan_rows, seconds: float = 12.0):
+    """The reference path on the host CPU: the oracle's restatement of
+    AxialReference.attend (fp32, additive -1e30 mask over all S keys) on a
+    bounded sample of config 3 -- one head, rows spread over every q-tile --
+    scaled to active-tile TFLOP/s so it reads in the metric's unit."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    row_ptr, col_idx = plan_rows
+    n = len(row_ptr) - 1
+    bm = np.zeros((n, n), dtype=np.uint8)
+    for i in range(n):
+        bm[i, col_idx[row_ptr[i]:row_ptr[i + 1]]] = 1
+    S, D = shape.seq_len, 128
+    rng = np.random.default_rng(0)
+    k = rng.standard_normal((S, D), dtype=np.float32)
+    v = rng.standard_normal((S, D), dtype=np.float32)
+    threads = min(16, os.cpu_count() or 1)
+
+    rows = np.arange(S, dtype=np.int32)
+    q = rng.standard_normal((S, D), dtype=np.float32)
+    row_len = np.diff(row_ptr).astype(np.int64)
+    head_flops = int(row_len[rows // 128].sum()) * 128 * D * 4   # active-tile FLOPs, one head
+
+    def one_head():
+        t0 = time.perf_counter()
+        O.attend_rows(q, rows, k, v, 1.0 / math.sqrt(D), bm, tile=128, threads=threads)
+        return time.perf_counter() - t0
+
+    first = one_head()
+    n_heads = int(max(1, min(shape.heads - 1, math.ceil(seconds / max(first, 1e-3)) - 1)))
+    dt = first + sum(one_head() for _ in range(n_heads))
+    n_heads += 1
+    return {
+        "value": round(n_heads * head_flops / dt / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle dense-masked attention (AxialReference.attend restated in C, "
+                   f"OpenMP, fp32, every query row scored against all {S} keys) on {n_heads} of "
+                   f"the {shape.heads} heads of config 3 in {dt:.1f} s; value = active-tile "
+                   f"FLOPs of those heads / time; a full layer would take "
+                   f"{dt / n_heads * shape.heads:.0f} s"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE "
+              f"{world}): the path shards by heads with no communication inside attention, "
+              f"so N GPUs run N independent copies of this measurement.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import h3hip
+    from h3hip import configs as C, ops
+
+    dev = torch.device("cuda:0")
+    shape = C.CFG3
+    S, S_pad, H, D = shape.seq_len, shape.seq_pad, shape.heads, C.HEAD_DIM
+    inner = H * D
+
+    # ---- plan (once per shape) --------------------------------------------
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan = h3hip.TilePlan(shape.mask_rule(), heads=H)
+    tile_build_ms = (time.perf_counter() - t0) * 1e3
+    t0 = time.perf_counter()
+    plan.close()
+    plan = h3hip.TilePlan(shape.mask_rule(), heads=H)
+    tile_build_ms = min(tile_build_ms, (time.perf_counter() - t0) * 1e3)
+    attn_flops = plan.nnz * H * FLOP_PER_TILE_HEAD
+
+    # ---- synthetic inputs, resident in HBM ----------------------------------
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    qkv = torch.randn((S, 3 * inner), generator=g, device=dev).to(torch.bfloat16)
+    gq = (torch.rand(D, generator=g, device=dev) * 0.2 + 0.9).to(torch.bfloat16)
+    gk = (torch.rand(D, generator=g, device=dev) * 0.2 + 0.9).to(torch.bfloat16)
+    pos = torch.from_numpy(ops.positions_grid(shape.prefix_len, shape.frames, shape.height,
+                                              shape.width)).to(dev)
+    ax_np, inv_np = ops.rope_pairs_axes(C.ROPE_THETA, C.ROPE_DIMS)
+    ax, inv = torch.from_numpy(ax_np).to(dev), torch.from_numpy(inv_np).to(dev)
+    qh = torch.empty((H, S_pad, D), dtype=torch.bfloat16, device=dev)
+    kh, vh = torch.empty_like(qh), torch.empty_like(qh)
+    out = torch.empty((S_pad, inner), dtype=torch.bfloat16, device=dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def prologue():
+        r = ops.qk_norm_rope(qkv[:, :inner], qkv[:, inner:2 * inner], gq, gk, pos, ax, inv,
+                             heads=H, eps=C.QK_EPS, seq_pad=S_pad, v_in=qkv[:, 2 * inner:],
+                             out=(qh, kh, vh))
+        assert r is not None
+
+    def attention():
+        r = ops.bsattn_fwd(plan, qh, kh, vh, scale, out_layout=h3hip.OUT_TOKEN_MAJOR, out=out)
+        assert r is not None
+
+    for _ in range(args.warmup):
+        prologue()
+        attention()
+    torch.cuda.synchronize()
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record()
+        prologue()
+        ev[i][1].record()
+        attention()
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    pro_ms = float(np.median([e[0].elapsed_time(e[1]) for e in ev]))
+    attn_ms = float(np.median([e[1].elapsed_time(e[2]) for e in ev]))
+    attn_mean_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+    ms_per_step = wall_ms / args.steps
+    attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
+    pro_bytes = 3 * S * inner * 2 + 3 * S_pad * inner * 2 + S * 12 + 2 * D * 2
+    pro_gbps = pro_bytes / (pro_ms * 1e-3) / 1e9
+    assert torch.isfinite(out[:S].float()).all()
+
+    result = {
+        "metric": METRIC,
+        "value": round(attn_tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded bf16 N(0,1) fused qkv [S, 3*5120], gamma U(0.9,1.1), integer (t,h,w) grid positions",
+        "config": {
+            "workload": shape.name,
+            "seq_len": S, "seq_pad": S_pad, "heads": H, "head_dim": D,
+            "video_grid": [shape.frames, shape.height, shape.width],
+            "text_tokens": shape.text, "audio_tokens": shape.audio,
+            "mask_rule": "local window: prefix rows/cols dense, +-1 latent frame, 3x3 spatial tiles of 8x8",
+            "active_tiles_per_head": plan.nnz, "tile_density": round(plan.density, 5),
+            "step": "prologue(Q,K norm+RoPE, V relayout) + block-sparse attention (token-major out)",
+        },
+        "attn_ms": round(attn_ms, 4),
+        "attn_ms_mean": round(attn_mean_ms, 4),
+        "attn_tflops_active": round(attn_tflops, 3),
+        "attn_mfma_peak_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+        "prologue_qkv_ms": round(pro_ms, 4),
+        "prologue_qkv_gbps": round(pro_gbps, 1),
+        "ms_per_layer": round(pro_ms + attn_ms, 4),
+        "tile_build_ms_once_per_shape": round(tile_build_ms, 2),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(attn_tflops, 3),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": read_traffic("bsattn_fwd_cfg3_traffic.txt"),
+        },
+    }
+
+    if not args.no_extras:
+        extras = {}
+        # Config 5: the prologue alone (Q, K only), fed by the hidden->Q,K setup GEMM.
+        hidden = torch.randn((S_pad, 5120), generator=g, device=dev).to(torch.bfloat16)
+        wq = (torch.randn((5120, inner), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        q_in = (hidden @ wq)[:S]
+        k_in = (hidden @ ((torch.randn((5120, inner), generator=g, device=dev) * 0.02)
+                          .to(torch.bfloat16)))[:S]
+        del hidden, wq
+        reps = max(10, args.steps)
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(reps + 3)]
+        for i, (a, b) in enumerate(evs):
+            a.record()
+            ops.qk_norm_rope(q_in, k_in, gq, gk, pos, ax, inv, heads=H, eps=C.QK_EPS,
+                             seq_pad=S_pad, out=(qh, kh, None))
+            b.record()
+        torch.cuda.synchronize()
+        p5 = float(np.median([a.elapsed_time(b) for a, b in evs[3:]]))
+        b5 = 2 * S * inner * 2 + 2 * S_pad * inner * 2 + S * 12 + 2 * D * 2
+        extras["cfg5_prologue_qk"] = {
+            "ms": round(p5, 4), "bytes": b5, "gbps": round(b5 / (p5 * 1e-3) / 1e9, 1),
+            "hbm_peak_frac": round(b5 / (p5 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            "traffic": read_traffic("qk_norm_rope_cfg5_traffic.txt"),
+        }
+        del q_in, k_in
+        for name in ("cfg3_1344x768x5s_frame0", "cfg2_864x480x7s", "cfg4_dense_864x480x7s"):
+            sh = C.ALL[name]
+            p = h3hip.TilePlan(sh.mask_rule(), heads=sh.heads)
+            qq = torch.randn((sh.heads, p.seq_pad, D), generator=g, device=dev).to(torch.bfloat16)
+            kk = torch.randn_like(qq)
+            vv = torch.randn_like(qq)
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(8)]
+            for a, b in evs:
+                a.record()
+                ops.bsattn_fwd(p, qq, kk, vv, scale)
+                b.record()
+            torch.cuda.synchronize()
+            ms = float(np.median([a.elapsed_time(b) for a, b in evs[2:]]))
+            fl = p.nnz * sh.heads * FLOP_PER_TILE_HEAD
+            extras[name] = {"attn_ms": round(ms, 4), "active_tiles_per_head": p.nnz,
+                            "density": round(p.density, 5),
+                            "tflops_active": round(fl / (ms * 1e-3) / 1e12, 3),
+                            "mfma_peak_frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+            del qq, kk, vv
+            p.close()
+        result["extras"] = extras
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(shape, plan.tiles())
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
