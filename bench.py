@@ -88,6 +88,37 @@ def cpu_baseline(shape, plan_rows, seconds: float = 12.0):
     }
 
 
+def profile_only(args, env) -> int:
+    """One kernel in isolation, for rocprofv3 counter runs."""
+    import torch
+    from h3hip import ops
+    dev, H, D, S, S_pad = env["dev"], env["H"], env["D"], env["S"], env["S_pad"]
+    if args.only == "copy":
+        src = torch.empty(1 << 29, dtype=torch.int16, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy: {args.steps} x {src.numel() * 2} bytes read and written")
+        return 0
+    if args.only == "attention":
+        env["prologue"]()
+        for _ in range(args.warmup + args.steps):
+            env["attention"]()
+        torch.cuda.synchronize()
+        print(f"attention: {args.steps} launches at {env['shape'].name}")
+        return 0
+    g, inner = env["g"], H * D
+    q_in = torch.randn((S, inner), generator=g, device=dev).to(torch.bfloat16)
+    k_in = torch.randn((S, inner), generator=g, device=dev).to(torch.bfloat16)
+    for _ in range(args.warmup + args.steps):
+        ops.qk_norm_rope(q_in, k_in, env["gq"], env["gk"], env["pos"], env["ax"], env["inv"],
+                         heads=H, eps=1e-6, seq_pad=S_pad, out=(env["qh"], env["kh"], None))
+    torch.cuda.synchronize()
+    print(f"prologue: {args.steps} launches, Q and K [{S}, {inner}] -> [{H}, {S_pad}, {D}]")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -95,6 +126,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--only", choices=("attention", "prologue", "copy"),
+                    help="profiling mode: run one kernel --steps times at config 3 (prologue: "
+                         "config 5, Q and K only; copy: a plain 1 GiB device copy for counter "
+                         "calibration) and print nothing but a one-line summary")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -149,6 +184,9 @@ def main() -> int:
     def attention():
         r = ops.bsattn_fwd(plan, qh, kh, vh, scale, out_layout=h3hip.OUT_TOKEN_MAJOR, out=out)
         assert r is not None
+
+    if args.only:
+        return profile_only(args, locals())
 
     for _ in range(args.warmup):
         prologue()

@@ -1,21 +1,30 @@
 // Fused Q/K RMSNorm + 3D split-half RoPE + relayout to head-major.
 //
-// Memory-bound: every (token, head) row of Q and K is read once (256 B each)
-// and written once, head-major. A workgroup owns TOKS consecutive tokens and
-// all heads; it first computes the rotation table (cos, sin of pos[axis] *
-// inv_freq for every pair) for its tokens into LDS -- once per token instead
-// of once per (token, head, tensor) -- then 16-lane groups stream the rows,
-// each lane holding 8 channels (one 16-byte load and store per tensor).
+// Memory-bound by design: every (token, head) row of Q and K is read once
+// (256 B) and written once, head-major. A workgroup owns kTok consecutive
+// tokens and all heads. It first computes the rotation table (cos, sin of
+// pos[axis] * inv_freq) for its tokens into LDS -- once per token, shared by
+// every head and by Q and K -- then 8-lane groups stream the rows: half of the
+// groups Q, half K, each with the next row's loads in flight.
+//
+// Lane ownership: lane j of a row holds two 8-channel chunks, chosen so that
+// each RoPE pair (p, p + rot/2) lives in one lane and the rotation needs no
+// cross-lane exchange: pair lanes (8j < rot/2) hold chunks j and j + rot/16;
+// the remaining lanes hold two consecutive pass-through chunks of the
+// channels >= rot. Each chunk is one 16-byte load and one 16-byte store.
 //
 // Arithmetic follows H3RMSNorm (Sources/H3Modules/Modulation.swift:116-120)
 // and SplitHalfRoPE (Sources/H3Modules/DiTBlock.swift:83-103):
-//   r = rsqrt(mean(x^2) + eps); y = bf16((x * r) * gamma)
-//   ra = bf16(bf16(c*a) + bf16(-s*b)); rb = bf16(bf16(s*a) + bf16(c*b))
-// with c, s = bf16(cos/sin(pos[axis] * inv_freq)) (the bf16 rotation table of
-// H3Transformer.swift:271-273). The sum of squares is accumulated in double:
-// squares of bf16 values are exact, so the mean is the exactly rounded fp32
-// mean whatever the reduction order; rsqrt and sin/cos are evaluated in
-// double and rounded once to fp32.
+//   ms = mean(x^2); r = rsqrt(ms + eps); y = (x * r) * gamma
+//   REFERENCE rounding: y, the table and every RoPE product and sum are
+//     rounded to bf16, as MLX computes the unfused chain on bf16 arrays:
+//     ra = bf16(bf16(c*a) + bf16(-s*b)), rb = bf16(bf16(s*a) + bf16(c*b)).
+//   FP32 rounding: fp32 throughout, one rounding at the store.
+// The mean is an fp32 sum in a fixed order: each lane accumulates its 16
+// squares with fma in channel order (chunk a, then chunk b), then the 8 lane
+// sums combine as t_j = s_j + s_{7-j}, u_j = t_j + t_{j^2}, total = u_j + u_{j^1}
+// (DPP half-row mirror, quad xor 2, quad xor 1); every lane ends with the same
+// bits. rsqrt is refined in double and rounded once to fp32.
 #include "common.h"
 
 namespace h3hip {
@@ -37,15 +46,26 @@ struct PrologueArgs {
   int32_t rot, seq_len, seq_pad, heads;
 };
 
-constexpr int kTok = 4;       // tokens per workgroup
+#ifndef H3HIP_PROLOGUE_TOK
+#define H3HIP_PROLOGUE_TOK 4
+#endif
+constexpr int kTok = H3HIP_PROLOGUE_TOK;  // tokens per workgroup
 constexpr int kHeadDim = 128;
 constexpr int kMaxHalf = 64;
+constexpr int kLanesPerRow = 8;
+constexpr int kRowGroups = 256 / kLanesPerRow;
 
 __device__ __forceinline__ u32x4 load16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
+// The row streams are touched once: non-temporal loads and stores keep them
+// from displacing reused lines (gamma, the table) and measure ~8% faster than
+// plain ones for a pure copy on MI355X.
+__device__ __forceinline__ u32x4 stream_load16(const uint16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 __device__ __forceinline__ void store16(uint16_t* p, u32x4 v) {
-  *reinterpret_cast<u32x4*>(p) = v;
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
 __device__ __forceinline__ void unpack8(u32x4 w, float* f) {
@@ -56,88 +76,143 @@ __device__ __forceinline__ void unpack8(u32x4 w, float* f) {
   }
 }
 
-__device__ __forceinline__ double group16_sum(double v) {
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off, 16);
-  return v;
+// Two fp32 values -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const f2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
 }
 
-// Normalises one row slice (8 channels per lane) and applies the rotation.
-// `j` is the lane's index inside its 16-lane group; channels 8j..8j+7.
-template <int kMode>
-__device__ __forceinline__ u32x4 norm_rope_row(u32x4 raw, const float* g, int j, int half,
-                                               int rot, float eps, const float2* cs) {
-  float x[8];
-  unpack8(raw, x);
-  double ss = 0.0;
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 r;
 #pragma unroll
-  for (int i = 0; i < 8; i++) ss += (double)x[i] * (double)x[i];
-  ss = group16_sum(ss);
-  const float ms = (float)(ss / (double)kHeadDim);
-  const float r = (float)(1.0 / sqrt((double)(ms + eps)));
-  float y[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) y[i] = (x[i] * r) * g[i];
+  for (int i = 0; i < 4; i++) r[i] = cvt_pk(f[2 * i], f[2 * i + 1]);
+  return r;
+}
 
-  const int hl = half >> 3;  // lanes per half
-  const int src = j < hl ? j + hl : (j < 2 * hl ? j - hl : j);
-  const bool is_a = j < hl, is_b = j >= hl && j < 2 * hl;
-  float out[8];
+// DPP controls used by the 8-lane reduction.
+constexpr int kDppHalfMirror = 0x141;   // lane j <- lane 7 - j within 8 lanes
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+
+// Rotation table entry for one pair: (c, s), bf16-rounded for REFERENCE
+// rounding (the bf16 table of H3Transformer.swift:271-273), fp32 otherwise.
+struct RopeEntry {
+  float c, s;
+};
+
+// 1/sqrt(x) rounded to fp32: the hardware estimate refined by one Newton step
+// in double (relative error ~1e-13 before the final rounding), i.e. the
+// correctly rounded value except within ~1e-13 of an fp32 rounding midpoint.
+__device__ __forceinline__ float rsqrt_rounded(float x) {
+  const double xd = (double)x, r0 = (double)__builtin_amdgcn_rsqf(x);
+  const double e = fma(-xd * r0, r0, 1.0);
+  return (float)fma(0.5 * r0, e, r0);
+}
+
+// Mean of squares of the row (fixed fp32 order, see the file header) and the
+// normalised values y = (x * r) * g.
+__device__ __forceinline__ void rms_normalise(const float* x, const float* g, float eps,
+                                              float* y) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) s = fmaf(x[i], x[i], s);
+  s = s + dpp<kDppHalfMirror>(s);
+  s = s + dpp<kDppQuadXor2>(s);
+  s = s + dpp<kDppQuadXor1>(s);
+  const float ms = s * (1.0f / kHeadDim);
+  const float r = rsqrt_rounded(ms + eps);
+#pragma unroll
+  for (int i = 0; i < 16; i++) y[i] = (x[i] * r) * g[i];
+}
+
+// One row slice: x holds chunk a (x[0..7]) and chunk b (x[8..15]). kFull:
+// every lane is a pair lane (rot == 128).
+template <int kMode, bool kFull>
+__device__ __forceinline__ void norm_rope(const float* x, const float* g, bool pair_lane,
+                                          const RopeEntry* tab, float eps, u32x4& out_a,
+                                          u32x4& out_b) {
+  float y[16];
+  rms_normalise(x, g, eps, y);
+  const bool rotate = kFull || pair_lane;
+  float oa[8], ob[8];
   if (kMode == H3HIP_ROUND_REFERENCE) {
-    u32x4 packed;
-#pragma unroll
-    for (int i = 0; i < 4; i++) packed[i] = pack_bf16x2(y[2 * i], y[2 * i + 1]);
-    u32x4 other;
-#pragma unroll
-    for (int i = 0; i < 4; i++) other[i] = __shfl(packed[i], src, 16);
-    float me[8], pt[8];
-    unpack8(packed, me);
-    unpack8(other, pt);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const int p = is_a ? 8 * j + i : 8 * j + i - half;
-      if (is_a) {
-        const float c = cs[p].x, s = cs[p].y;
-        out[i] = round_bf16(round_bf16(c * me[i]) + round_bf16(-s * pt[i]));
-      } else if (is_b) {
-        const float c = cs[p].x, s = cs[p].y;
-        out[i] = round_bf16(round_bf16(s * pt[i]) + round_bf16(c * me[i]));
-      } else {
-        out[i] = me[i];
-      }
+      const uint32_t ab = cvt_pk(y[i], y[8 + i]);  // bf16(y_a) | bf16(y_b)
+      const float a = bf16_lo(ab), b = bf16_hi(ab);
+      const float c = tab[i].c, sn = tab[i].s;
+      const uint32_t p1 = cvt_pk(c * a, -sn * b);
+      const uint32_t p2 = cvt_pk(sn * a, c * b);
+      const float ra = bf16_lo(p1) + bf16_hi(p1);
+      const float rb = bf16_lo(p2) + bf16_hi(p2);
+      oa[i] = rotate ? ra : a;
+      ob[i] = rotate ? rb : b;
     }
   } else {
-    float pt[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) pt[i] = __shfl(y[i], src, 16);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const int p = is_a ? 8 * j + i : 8 * j + i - half;
-      if (is_a) {
-        const float c = cs[p].x, s = cs[p].y;
-        out[i] = c * y[i] - s * pt[i];
-      } else if (is_b) {
-        const float c = cs[p].x, s = cs[p].y;
-        out[i] = s * pt[i] + c * y[i];
-      } else {
-        out[i] = y[i];
-      }
+      const float c = tab[i].c, sn = tab[i].s;
+      const float ra = c * y[i] - sn * y[8 + i];
+      const float rb = sn * y[i] + c * y[8 + i];
+      oa[i] = rotate ? ra : y[i];
+      ob[i] = rotate ? rb : y[8 + i];
     }
   }
-  u32x4 res;
-#pragma unroll
-  for (int i = 0; i < 4; i++) res[i] = pack_bf16x2(out[2 * i], out[2 * i + 1]);
-  return res;
+  out_a = pack8(oa);
+  out_b = pack8(ob);
 }
 
-template <int kMode>
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
-  __shared__ float2 cs[kTok][kMaxHalf];
+// Workgroup: kTok tokens x all heads. Row groups of 8 lanes; the first half of
+// the groups normalise Q rows, the second half K rows, each streaming its rows
+// with the next row's loads issued before the current row is computed. V rows
+// (when given) are copied by all groups afterwards.
+template <int kMode, bool kFull>
+__global__ __launch_bounds__(256, 5) void qk_norm_rope_kernel(PrologueArgs a) {
+  __shared__ RopeEntry tab_lds[kTok][kMaxHalf];
   const int tid = threadIdx.x;
   const int32_t s0 = blockIdx.x * kTok;
   const int half = a.rot >> 1;
 
-  // Rotation table for this workgroup's tokens.
+  const int grp = tid / kLanesPerRow, j = tid % kLanesPerRow;
+  const int hl = half / 8;  // pair lanes per row
+  const bool pair_lane = kFull || j < hl;
+  const int chunk_a = pair_lane ? j : 2 * hl + 2 * (j - hl);
+  const int chunk_b = pair_lane ? j + hl : chunk_a + 1;
+  const int off_a = 8 * chunk_a, off_b = 8 * chunk_b;
+  const int pair0 = pair_lane ? 8 * j : 0;
+
+  constexpr int kGroupsPerTensor = kRowGroups / 2;
+  const bool is_k = grp >= kGroupsPerTensor;
+  const int g0 = is_k ? grp - kGroupsPerTensor : grp;
+  const uint16_t* __restrict__ in = is_k ? a.k_in : a.q_in;
+  uint16_t* __restrict__ out = is_k ? a.k_out : a.q_out;
+  float gam[16];
+  {
+    const uint16_t* gsrc = is_k ? a.k_gamma : a.q_gamma;
+    unpack8(load16(gsrc + off_a), gam);
+    unpack8(load16(gsrc + off_b), gam + 8);
+  }
+
+  const int rows = kTok * a.heads;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  auto src_of = [&](int rho) {
+    const int head = rho / kTok, tok = rho - head * kTok;
+    return (int64_t)(s0 + tok) * a.ld_in + (int64_t)head * kHeadDim;
+  };
+  auto valid = [&](int rho) { return rho < rows && s0 + (rho % kTok) < a.seq_len; };
+  u32x4 na = zero, nb = zero;
+  if (valid(g0)) {
+    na = stream_load16(in + src_of(g0) + off_a);
+    nb = stream_load16(in + src_of(g0) + off_b);
+  }
+  // The first row is in flight while the rotation table is computed.
   for (int t = tid; t < kTok * half; t += 256) {
     const int tok = t / half, p = t - tok * half;
     const int32_t s = s0 + tok;
@@ -145,42 +220,51 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     if (s < a.seq_len) {
       const int axis = min(max(a.pair_axis[p], 0), 2);  // a bad table cannot index past pos
       const float ang = a.pos[(int64_t)s * 3 + axis] * a.pair_inv[p];
-      c = (float)cos((double)ang);
-      sn = (float)sin((double)ang);
-      if (kMode == H3HIP_ROUND_REFERENCE) {
-        c = round_bf16(c);
-        sn = round_bf16(sn);
-      }
+      sincosf(ang, &sn, &c);
     }
-    cs[tok][p] = make_float2(c, sn);
+    if (kMode == H3HIP_ROUND_REFERENCE) {
+      c = round_bf16(c);
+      sn = round_bf16(sn);
+    }
+    tab_lds[tok][p] = RopeEntry{c, sn};
   }
 
-  const int g = tid >> 4, j = tid & 15;
-  float qg[8], kg[8];
-  unpack8(load16(a.q_gamma + 8 * j), qg);
-  unpack8(load16(a.k_gamma + 8 * j), kg);
   __syncthreads();
 
-  const int rows = kTok * a.heads;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  for (int rho = g; rho < rows; rho += 16) {
+  for (int rho = g0; rho < rows; rho += kGroupsPerTensor) {
+    const u32x4 ca = na, cb = nb;
+    const int next = rho + kGroupsPerTensor;
+    if (valid(next)) {
+      na = stream_load16(in + src_of(next) + off_a);
+      nb = stream_load16(in + src_of(next) + off_b);
+    }
     const int head = rho / kTok, tok = rho - head * kTok;
     const int32_t s = s0 + tok;
-    const int64_t dst = ((int64_t)head * a.seq_pad + s) * kHeadDim + 8 * j;
-    if (s >= a.seq_len) {
-      store16(a.q_out + dst, zero);
-      store16(a.k_out + dst, zero);
-      if (a.v_out) store16(a.v_out + dst, zero);
-      continue;
+    uint16_t* dst = out + ((int64_t)head * a.seq_pad + s) * kHeadDim;
+    u32x4 oa = zero, ob = zero;
+    if (s < a.seq_len) {
+      float x[16];
+      unpack8(ca, x);
+      unpack8(cb, x + 8);
+      norm_rope<kMode, kFull>(x, gam, pair_lane, &tab_lds[tok][pair0], a.eps, oa, ob);
     }
-    const int64_t src = (int64_t)s * a.ld_in + (int64_t)head * kHeadDim + 8 * j;
-    const u32x4 qraw = load16(a.q_in + src);
-    const u32x4 kraw = load16(a.k_in + src);
-    u32x4 vraw = zero;
-    if (a.v_in) vraw = load16(a.v_in + src);
-    store16(a.q_out + dst, norm_rope_row<kMode>(qraw, qg, j, half, a.rot, a.eps, cs[tok]));
-    store16(a.k_out + dst, norm_rope_row<kMode>(kraw, kg, j, half, a.rot, a.eps, cs[tok]));
-    if (a.v_in) store16(a.v_out + dst, vraw);
+    store16(dst + off_a, oa);
+    store16(dst + off_b, ob);
+  }
+
+  if (a.v_in) {
+    for (int rho = grp; rho < rows; rho += kRowGroups) {
+      const int head = rho / kTok, tok = rho - head * kTok;
+      const int32_t s = s0 + tok;
+      uint16_t* dst = a.v_out + ((int64_t)head * a.seq_pad + s) * kHeadDim;
+      u32x4 va = zero, vb = zero;
+      if (s < a.seq_len) {
+        va = stream_load16(a.v_in + src_of(rho) + off_a);
+        vb = stream_load16(a.v_in + src_of(rho) + off_b);
+      }
+      store16(dst + off_a, va);
+      store16(dst + off_b, vb);
+    }
   }
 }
 
@@ -215,7 +299,8 @@ extern "C" int h3hip_qk_norm_rope(const void* q_in, const void* k_in, int64_t ld
              "unknown rounding mode %d", rounding);
   auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   H3_REQUIRE(aligned16(q_in) && aligned16(k_in) && aligned16(q_gamma) && aligned16(k_gamma) &&
-                 aligned16(q_out) && aligned16(k_out) && (!v_in || (aligned16(v_in) && aligned16(v_out))),
+                 aligned16(q_out) && aligned16(k_out) &&
+                 (!v_in || (aligned16(v_in) && aligned16(v_out))),
              H3HIP_EINVAL, "tensors must be 16-byte aligned");
   PrologueArgs a{static_cast<const uint16_t*>(q_in),   static_cast<const uint16_t*>(k_in),
                  static_cast<const uint16_t*>(v_in),   static_cast<const uint16_t*>(q_gamma),
@@ -227,9 +312,18 @@ extern "C" int h3hip_qk_norm_rope(const void* q_in, const void* k_in, int64_t ld
                  seq_len,                               seq_pad,
                  heads};
   const dim3 grid(seq_pad / kTok);
-  if (rounding == H3HIP_ROUND_REFERENCE)
-    qk_norm_rope_kernel<H3HIP_ROUND_REFERENCE><<<grid, 256, 0, as_stream(stream)>>>(a);
-  else
-    qk_norm_rope_kernel<H3HIP_ROUND_FP32><<<grid, 256, 0, as_stream(stream)>>>(a);
+  hipStream_t st = as_stream(stream);
+  const bool full = rot == head_dim;
+  if (rounding == H3HIP_ROUND_REFERENCE) {
+    if (full)
+      qk_norm_rope_kernel<H3HIP_ROUND_REFERENCE, true><<<grid, 256, 0, st>>>(a);
+    else
+      qk_norm_rope_kernel<H3HIP_ROUND_REFERENCE, false><<<grid, 256, 0, st>>>(a);
+  } else {
+    if (full)
+      qk_norm_rope_kernel<H3HIP_ROUND_FP32, true><<<grid, 256, 0, st>>>(a);
+    else
+      qk_norm_rope_kernel<H3HIP_ROUND_FP32, false><<<grid, 256, 0, st>>>(a);
+  }
   return check_launch("qk_norm_rope_kernel");
 }

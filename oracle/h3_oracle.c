@@ -358,7 +358,9 @@ void orc_attend_streaming(const float* q, const float* k, const float* v,
 
 /* H3RMSNorm then SplitHalfRoPE, per (token, head) row:
  *   H3RMSNorm (Sources/H3Modules/Modulation.swift:116-120):
- *     f = fp32(x); n = f * rsqrt(mean(f*f) + eps); y = bf16(n * fp32(gamma))
+ *     f = fp32(x); n = f * rsqrt(mean(f*f) + eps); y = bf16(n * fp32(gamma)),
+ *     the mean in the fixed order of mean_square_fixed_order (D == 128),
+ *     rsqrt in double rounded once to fp32
  *   RoPE angle (Sources/H3Modules/H3Transformer.swift:66-78):
  *     angle = fp32(pos[axis]) * inv_freq (fp32); table = bf16([[c,-s],[s,c]]),
  *     c and s the fp32-rounded cos/sin of the fp32 angle
@@ -369,6 +371,28 @@ void orc_attend_streaming(const float* q, const float* k, const float* v,
  *   pairs (p, p + rot/2), channels >= rot pass through.
  * ORC_ROUND_FP32 keeps the normalised row and the rotation in fp32 and rounds
  * once at the store. Output is head-major [H, S_pad, D]; rows >= S are zero. */
+/* The mean of squares over a 128-channel row in the fixed fp32 order the
+ * prologue defines (the reference's MLX reduction order is not observable):
+ * the row is split into 8 pieces of two 8-channel chunks -- piece j holds
+ * chunks j and j + rot/16 while 8j < rot/2, else two consecutive chunks of the
+ * channels >= rot -- each piece is summed with fma in channel order, and the 8
+ * piece sums combine as t_j = s_j + s_{7-j}, u_j = t_j + t_{j^2}, u_0 + u_1. */
+static float mean_square_fixed_order(const float* f, int32_t rot) {
+  const int32_t hl = rot / 16;
+  float sj[8];
+  for (int32_t j = 0; j < 8; j++) {
+    int32_t ca = j < hl ? j : 2 * hl + 2 * (j - hl);
+    int32_t cb = j < hl ? j + hl : ca + 1;
+    float acc = 0.f;
+    for (int32_t i = 0; i < 8; i++) acc = fmaf(f[8 * ca + i], f[8 * ca + i], acc);
+    for (int32_t i = 0; i < 8; i++) acc = fmaf(f[8 * cb + i], f[8 * cb + i], acc);
+    sj[j] = acc;
+  }
+  float t0 = sj[0] + sj[7], t1 = sj[1] + sj[6], t2 = sj[2] + sj[5], t3 = sj[3] + sj[4];
+  float u0 = t0 + t2, u1 = t1 + t3;
+  return (u0 + u1) * (1.0f / 128.0f);
+}
+
 void orc_qk_norm_rope(const uint16_t* x, int64_t ld, int32_t S, int32_t S_pad,
                       int32_t H, int32_t D, const uint16_t* gamma, float eps,
                       const float* pos, const int32_t* pair_axis, const float* pair_inv,
@@ -390,12 +414,8 @@ void orc_qk_norm_rope(const uint16_t* x, int64_t ld, int32_t S, int32_t S_pad,
         continue;
       }
       const uint16_t* xr = x + (int64_t)s * ld + (int64_t)h * D;
-      double ss = 0.0; /* squares of bf16 values are exact: the sum is order-free */
-      for (int32_t d = 0; d < D; d++) {
-        f[d] = orc_bf16_to_f32(xr[d]);
-        ss += (double)f[d] * f[d];
-      }
-      float ms = (float)(ss / D);
+      for (int32_t d = 0; d < D; d++) f[d] = orc_bf16_to_f32(xr[d]);
+      float ms = mean_square_fixed_order(f, rot);
       float r = (float)(1.0 / sqrt((double)(ms + eps)));
       for (int32_t d = 0; d < D; d++) y[d] = (f[d] * r) * orc_bf16_to_f32(gamma[d]);
       for (int32_t d = 0; d < D; d++) o[d] = orc_f32_to_bf16(y[d]);

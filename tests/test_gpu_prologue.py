@@ -87,6 +87,7 @@ def test_prologue_matches_oracle(h3, orc, S, H, rot, rounding, h3t):
     for name in ("q", "k"):
         got, want = res[name]
         rel, ulp, same = gate(got, want)
+        print(f"{name}: rel {rel:.2e} ulp {ulp:.2f} identical {same:.6f}")
         assert rel < 1e-3 and ulp < 8, (name, rel, ulp)
         if rounding == 0:
             assert same >= 0.999, (name, same)

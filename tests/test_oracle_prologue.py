@@ -8,12 +8,28 @@ import numpy as np
 import pytest
 
 
+def numpy_mean_square(x, rot):
+    """The prologue's fixed fp32 reduction order, vectorised over rows."""
+    hl = rot // 16
+    sj = []
+    for j in range(8):
+        ca = j if j < hl else 2 * hl + 2 * (j - hl)
+        cb = j + hl if j < hl else ca + 1
+        acc = np.zeros(x.shape[:-1], dtype=np.float32)
+        for c in (ca, cb):
+            for i in range(8):
+                v = x[..., 8 * c + i].astype(np.float64)
+                acc = (v * v + acc.astype(np.float64)).astype(np.float32)   # fma: one rounding
+        sj.append(acc)
+    t = [sj[0] + sj[7], sj[1] + sj[6], sj[2] + sj[5], sj[3] + sj[4]]
+    return (((t[0] + t[2]) + (t[1] + t[3])) * np.float32(1.0 / 128.0))[..., None]
+
+
 def numpy_reference_prologue(orc, x_bits, S, H, D, gamma_bits, eps, pos, axis, inv, rot):
     """Row-vectorised restatement with the reference's bf16 rounding points."""
     x = orc.bf16_to_f32(x_bits).reshape(S, H, D)
     g = orc.bf16_to_f32(gamma_bits)
-    ss = np.sum(x.astype(np.float64) ** 2, axis=-1, keepdims=True)
-    ms = (ss / D).astype(np.float32)
+    ms = numpy_mean_square(x, rot)
     r = (1.0 / np.sqrt((ms + np.float32(eps)).astype(np.float64))).astype(np.float32)
     y = ((x * r).astype(np.float32) * g).astype(np.float32)
     yb = orc.bf16_to_f32(orc.f32_to_bf16(y))
@@ -58,8 +74,8 @@ def test_position_zero_is_identity_and_tail_passes_through(orc):
     normed = orc.qk_norm_rope(x, H * D, S, S, H, D, gamma, 1e-6, pos, axis, inv, 96)
     # At position 0 every rotation is the identity: the output is bf16(y).
     xf = orc.bf16_to_f32(x).reshape(S, H, D)
-    r = (1.0 / np.sqrt(((np.sum(xf.astype(np.float64) ** 2, -1, keepdims=True) / D)
-                        .astype(np.float32) + np.float32(1e-6)).astype(np.float64))).astype(np.float32)
+    r = (1.0 / np.sqrt((numpy_mean_square(xf, 96) + np.float32(1e-6))
+                       .astype(np.float64))).astype(np.float32)
     y = orc.f32_to_bf16(((xf * r).astype(np.float32) * orc.bf16_to_f32(gamma)).astype(np.float32))
     assert np.array_equal(normed, y.transpose(1, 0, 2))
     # Channels >= rot pass through bit-exactly at any position.
