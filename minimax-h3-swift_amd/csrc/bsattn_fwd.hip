@@ -1,20 +1,28 @@
 // Block-sparse flash attention over 128x128 tiles, bf16 MFMA on gfx950.
 //
-// One workgroup (4 waves) per (head, 128-query tile) work unit, launched in
-// the plan's XCD-aware order. Each wave owns 32 queries and keeps them in
-// registers as the B operand of v_mfma_f32_32x32x16_bf16. Per active key tile
-// the workgroup stages K (row-major) and V (transposed, V^T) in LDS, then each
-// wave computes the transposed scores S^T = K Q^T, so a lane holds one
-// query's scores for 32 keys: the row max and row sum are in-register
-// reductions plus one exchange between the two half-waves, not a 32-lane
-// shuffle tree. The exponentiated scores are already laid out as the B
-// operand of O^T = V^T P^T (the 16-key chunk k of the MFMA pairs the C
-// layout's register groups), so P never leaves registers.
+// One workgroup of 8 waves per (head, 128-query tile) work unit, one
+// workgroup per CU, launched in the plan's XCD-aware order. Waves w and w+4
+// own the same 32 queries (the B operand of v_mfma_f32_32x32x16_bf16, kept in
+// registers) and split every key tile in two 64-key halves, each keeping its
+// own online-softmax state; the halves are merged exactly at the end. The two
+// waves of a pair share a SIMD and run a ping-pong schedule (see the kernel),
+// so one's softmax overlaps the other's MFMAs.
+//
+// Each wave computes transposed scores S^T = K Q^T, so a lane holds one
+// query's scores and the row max/sum are in-register reductions plus one
+// exchange between half-waves. The exponentiated scores are already the B
+// operand of O^T = V^T P^T; the A operand V^T is read from the row-major V
+// tile with ds_read_b64_tr_b16, whose 16-lane transpose hands lane i column
+// c0+i of four consecutive rows.
 //
 // The softmax is the online recurrence of AxialReference.attendStreamingKeys
 // (Sources/H3Attention/AxialReference.swift:129-171) in fp32 and base 2:
-// m starts at -3e38, keys >= seq_len take the -1e30 sentinel, l and O are
-// rescaled by 2^(m - m_new) per tile, and the output is O / max(l, 1e-30).
+// m starts at -3e38, keys >= seq_len take the -1e30 sentinel, and l and O
+// are rescaled by 2^(m - m_new) when the running max moves. The rescale is
+// lazy: m is only raised when a tile's max exceeds it by more than 2^8, which
+// keeps every exponentiated score <= 256 and changes nothing in exact
+// arithmetic (numerator and denominator share m). The output is
+// O / max(l, 1e-30).
 #include <cmath>
 
 #include "common.h"
@@ -24,11 +32,16 @@ namespace h3hip {
 
 constexpr int kTile = 128;
 constexpr int kD = 128;
-// LDS row strides (bf16 elements). K rows are read 16 B at a time by 32
-// consecutive rows: 272-byte rows put the 8 lanes of a phase on distinct
-// banks. V^T rows are read 8 B at a time: 264-byte rows do the same for 16.
-constexpr int kKStride = 136;
-constexpr int kVStride = 132;
+constexpr int kThreads = 512;
+constexpr int kSlot = kTile * kD;                   // one K or V tile, unpadded
+constexpr float kRescaleSlack = 8.0f;              // log2 units
+// s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt left unconstrained
+// (gfx9 encoding: vmcnt[3:0] bits 3:0, expcnt bits 6:4, lgkmcnt bits 11:8,
+// vmcnt[5:4] bits 15:14).
+constexpr int kWaitVmcnt0 = 0x0F70;
+// Buffer resource word 3 for raw (untyped, unswizzled) buffer loads on gfx9:
+// DATA_FORMAT = 32 bits, everything else zero.
+constexpr int kBufferWord3 = 0x00020000;
 
 struct AttnArgs {
   const uint16_t* __restrict__ q;
@@ -42,28 +55,68 @@ struct AttnArgs {
   float scale_log2;
 };
 
-__device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(1))) void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// LDS tiles are unpadded 256-byte rows whose 16-byte chunks are XOR-swizzled
+// so the operand reads hit 64 distinct banks per phase:
+//   K: chunk c of row r sits at c ^ (r & 15) -- 16 consecutive rows read at
+//      one chunk (ds_read_b128) land on 16 different chunk positions;
+//   V: chunk c of row r sits at c ^ (4*(r & 3) + ((r >> 2) & 3)) -- the
+//      transpose load reads 4 consecutive rows x 4 consecutive chunks per
+//      32-lane phase, which this maps onto all 16 chunk positions.
+__device__ __forceinline__ int k_swz(int r) { return r & 15; }
+__device__ __forceinline__ int v_swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
+
+// Eight bf16 of V^T for the A operand: two transpose loads of 4 rows each.
+__device__ __forceinline__ bf16x8 vt_operand(const uint16_t* p0, const uint16_t* p1) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, w);
 }
 
-__device__ __forceinline__ uint32_t half_of(uint32_t w, int hi) {
-  return hi ? (w >> 16) : (w & 0xffffu);
+__device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& s, int base) {
+  typedef float f32x8 __attribute__((ext_vector_type(8)));
+  const f32x8 v = {s[base], s[base + 1], s[base + 2], s[base + 3],
+                   s[base + 4], s[base + 5], s[base + 6], s[base + 7]};
+  return __builtin_convertvector(v, bf16x8);
 }
 
-__global__ __launch_bounds__(256, 2) void bsattn_fwd_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[kTile * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[kD * kVStride];
+// Workgroup: 8 waves, one (head, 128-query tile) unit. Wave w owns queries
+// 32*(w&3) .. +31 and key half (w>>2) (keys 64*(w>>2) .. +63) of every tile.
+//
+// Ping-pong schedule. Each wave alternates an MFMA phase M_j -- the scores
+// S(j) = K(j) Q^T of tile j and the product O += V(j-1)^T P(j-1) of the
+// previous tile -- with a VALU phase V_j -- the online softmax of S(j) into
+// P(j). Waves 4-7 run one phase behind waves 0-3, and every phase ends in a
+// workgroup barrier, so on each SIMD one wave of the pair is issuing MFMAs
+// while the other is in its softmax.
+//
+// Data movement is direct HBM -> LDS (global_load_lds, no registers), issued
+// only by the waves in their softmax phase, which drain it before the phase
+// barrier: waves 4-7 load K(j+1) in phase 2j, waves 0-3 load V(j) in phase
+// 2j+1, and both are consumed from phase 2j+2 on. K(j+1) replaces K(j-1) and
+// V(j) replaces V(j-2), both last read before phase 2j. The MFMA waves thus
+// never have a load in flight, and their LDS operand reads wait for nothing.
+__global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
+  // Slots: K(j) at (j & 1) * kSlot, V(j) at (2 + (j & 1)) * kSlot; 128 KiB.
+  __shared__ __attribute__((aligned(16))) uint16_t lds[4 * kSlot];
 
   const int32_t unit = a.work[blockIdx.x];
   if (unit < 0) return;
   const int head = unit >> 16, qt = unit & 0xffff;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
+  const int qg = wave & 3, half = wave >> 2;
   const int li = lane & 31, hh = lane >> 5;
   const size_t head_off = (size_t)head * a.seq_pad * kD;
   const uint16_t* qh = a.q + head_off;
-  const uint16_t* kh = a.k + head_off;
-  const uint16_t* vh = a.v + head_off;
-  const int q0 = qt * kTile + wave * 32;
+  const int q0 = qt * kTile + qg * 32;
+  const float c = a.scale_log2;
 
   // Q^T as the B operand: lane (li, hh) holds Q[q0 + li][16s + 8hh .. +7].
   bf16x8 qreg[8];
@@ -73,123 +126,204 @@ __global__ __launch_bounds__(256, 2) void bsattn_fwd_kernel(AttnArgs a) {
     for (int s = 0; s < 8; s++) qreg[s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
   }
 
+  // K operand offsets: block b row half*64 + 32b + li, chunk 2s + hh.
+  int k_off[8];
+#pragma unroll
+  for (int s = 0; s < 8; s++) k_off[s] = (half * 64 + li) * kD + (((2 * s + hh) ^ k_swz(li)) * 8);
+  // V^T operand offsets: lane (g = lane/16, m = lane%16) points at row
+  // half*64 + 16kc + 8p + 4(g/2) + m/4, element 32db + 16(g%2) + 4(m%4).
+  const int g = lane >> 4, mm = lane & 15;
+  int v_off[2][4];
+#pragma unroll
+  for (int p = 0; p < 2; p++)
+#pragma unroll
+    for (int db = 0; db < 4; db++) {
+      const int row = half * 64 + 8 * p + 4 * (g >> 1) + (mm >> 2);
+      const int chunk = 4 * db + 2 * (g & 1) + ((mm & 3) >> 1);
+      v_off[p][db] = row * kD + ((chunk ^ v_swz(row)) * 8) + 4 * (mm & 1);
+    }
+
+  // HBM -> LDS by one half of the workgroup, as buffer loads (a per-head
+  // resource, the key offset in an SGPR, 32-bit lane offsets): wave w moves
+  // rows 32(w&3) .. +31 of a tile, 4 rows per instruction; lane l fills chunk
+  // position l%16 of row 32(w&3) + 4i + l/16 from the global chunk that the
+  // swizzle places there.
+  const int head_bytes = a.seq_pad * kD * 2;
+  const __amdgpu_buffer_rsrc_t k_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.k + head_off), 0, head_bytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t v_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.v + head_off), 0, head_bytes, kBufferWord3);
+  const int dma_row = 32 * qg + (lane >> 4);
+  auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int key0, uint16_t* slot,
+                 bool v_layout) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int row = dma_row + 4 * i;
+      const int swz = v_layout ? v_swz(row) : k_swz(row);
+      const int voff = row * (kD * 2) + (((lane & 15) ^ swz) * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, (lds_void*)(slot + (32 * qg + 4 * i) * kD), 16, voff, key0 * (kD * 2), 0, 0);
+    }
+  };
+
   f32x16 oacc[4];
 #pragma unroll
   for (int db = 0; db < 4; db++)
 #pragma unroll
     for (int r = 0; r < 16; r++) oacc[db][r] = 0.f;
   float m = -3.0e38f, l = 0.f;
+  f32x16 sacc[2];
+  bf16x8 pb[4];
 
-  const int beg = a.row_ptr[qt], end = a.row_ptr[qt + 1];
-  const int k_row = tid >> 4, k_col = (tid & 15) * 8;
-  const int v_d0 = (tid >> 4) * 8, v_j0 = (tid & 15) * 8;
+  const int beg = a.row_ptr[qt], n = a.row_ptr[qt + 1] - beg;
+  // Column indices through the constant address space: scalar loads.
+  const __attribute__((address_space(4))) int32_t* cols =
+      (const __attribute__((address_space(4))) int32_t*)(a.col_idx) + beg;
 
-  for (int t = beg; t < end; t++) {
-    const int key0 = a.col_idx[t] * kTile;
-    __syncthreads();  // the previous tile's LDS reads are done
+  // M_j: S(j) = K(j) Q^T and O += V(j-1)^T P(j-1).
+  auto m_phase = [&](int j) __attribute__((always_inline)) {
+    if (j < n) {
+      const uint16_t* kb = lds + (j & 1) * kSlot;
 #pragma unroll
-    for (int it = 0; it < 8; it++) {
-      const int row = it * 16 + k_row;
-      *reinterpret_cast<u32x4*>(ks + row * kKStride + k_col) =
-          ld16(kh + (size_t)(key0 + row) * kD + k_col);
-    }
-    {
-      // 8 keys x 8 channels per thread, transposed in registers, written as
-      // V^T[d0 + c][j0 .. j0 + 7]. Keys >= seq_len load as zero.
-      u32x4 vr[8];
+      for (int b = 0; b < 2; b++)
 #pragma unroll
-      for (int r = 0; r < 8; r++) {
-        const int key = key0 + v_j0 + r;
-        vr[r] = key < a.seq_len ? ld16(vh + (size_t)key * kD + v_d0) : u32x4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int c = 0; c < 8; c++) {
-        u32x2 w0, w1;
-        w0[0] = half_of(vr[0][c >> 1], c & 1) | (half_of(vr[1][c >> 1], c & 1) << 16);
-        w0[1] = half_of(vr[2][c >> 1], c & 1) | (half_of(vr[3][c >> 1], c & 1) << 16);
-        w1[0] = half_of(vr[4][c >> 1], c & 1) | (half_of(vr[5][c >> 1], c & 1) << 16);
-        w1[1] = half_of(vr[6][c >> 1], c & 1) | (half_of(vr[7][c >> 1], c & 1) << 16);
-        uint16_t* dst = vt + (v_d0 + c) * kVStride + v_j0;
-        *reinterpret_cast<u32x2*>(dst) = w0;
-        *reinterpret_cast<u32x2*>(dst + 4) = w1;
-      }
-    }
-    __syncthreads();
-
-    // S^T[key][query] for the wave's 32 queries: 4 blocks of 32 keys.
-    f32x16 sacc[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; kb++) {
-#pragma unroll
-      for (int r = 0; r < 16; r++) sacc[kb][r] = 0.f;
-      const uint16_t* krow = ks + (32 * kb + li) * kKStride + 8 * hh;
+        for (int r = 0; r < 16; r++) sacc[b][r] = 0.f;
 #pragma unroll
       for (int s = 0; s < 8; s++) {
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(krow + 16 * s);
-        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[s], sacc[kb], 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kb + k_off[s] + b * 32 * kD);
+          sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[s], sacc[b], 0, 0, 0);
+        }
       }
     }
-    if (key0 + kTile > a.seq_len) {
+    if (j >= 1) {
+      const uint16_t* vb = lds + (2 + ((j - 1) & 1)) * kSlot;
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++)
+      for (int kc = 0; kc < 4; kc++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int key = key0 + 32 * kb + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key >= a.seq_len) sacc[kb][r] = -1.0e30f;
+        for (int db = 0; db < 4; db++) {
+          const bf16x8 va = vt_operand(vb + v_off[0][db] + 16 * kc * kD,
+                                       vb + v_off[1][db] + 16 * kc * kD);
+          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kc], oacc[db], 0, 0, 0);
         }
     }
+  };
 
+  // V_j: online softmax of S(j) into P(j) (bf16 B operands).
+  auto v_phase = [&](int j) __attribute__((always_inline)) {
+    const int key0 = cols[j] * kTile;
+    if (key0 + kTile > a.seq_len) {
+#pragma unroll
+      for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int key = key0 + half * 64 + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
+          if (key >= a.seq_len) sacc[b][r] = -1.0e30f;
+        }
+    }
     float mx = -3.0e38f;
 #pragma unroll
-    for (int kb = 0; kb < 4; kb++)
+    for (int b = 0; b < 2; b++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[kb][r]);
+      for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[b][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx * a.scale_log2);
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    const float m_cand = fmaxf(m, mx * c);
+    const bool raise = m_cand > m + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+      const float m_new = raise ? m_cand : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; db++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) oacc[db][r] *= alpha;
+    }
     float psum = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 4; kb++)
+    for (int b = 0; b < 2; b++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][r], a.scale_log2, -m_new));
-        sacc[kb][r] = p;
-        psum += p;
+        const float e = __builtin_amdgcn_exp2f(fmaf(sacc[b][r], c, -m));
+        sacc[b][r] = e;
+        psum += e;
       }
-    l = l * alpha + psum;
-    m = m_new;
+    l += psum;
+    // Chunk kc of P^T: registers 8*(kc&1) .. +7 of block kc>>1; element e of
+    // half-wave hh is key 16kc + 8(e/4) + 4hh + e%4, matching the rows the
+    // two transpose loads of the V^T operand fetch.
 #pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) oacc[db][r] *= alpha;
+    for (int kc = 0; kc < 4; kc++) pb[kc] = to_bf16x8(sacc[kc >> 1], 8 * (kc & 1));
+  };
 
-    // P^T as the B operand of O^T = V^T P^T: chunk kc takes registers
-    // 8*(kc&1) .. +7 of key block kc>>1; element e of half-wave hh is key
-    // 16kc + 8(e/4) + 4hh + e%4, so V^T supplies keys 16kc+4hh+[0,4) and
-    // 16kc+8+4hh+[0,4) in the same element order.
-    bf16x8 pb[8];
+  if (n > 0) {
+    // K(0) by waves 0-3; the Q loads drain with it.
+    if (half == 0) dma(k_rsrc, cols[0] * kTile, lds, false);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    // Each half runs its own loop of two phases per tile (2n + 2 phases and
+    // barriers in all), so neither loop merges the other role's state.
+    if (half == 0) {
+      for (int j = 0; j <= n; j++) {
+        m_phase(j);                                       // phase 2j
+        __syncthreads();
+        if (j < n) {                                      // phase 2j + 1
+          const int key0 = cols[j] * kTile;
+          uint16_t* vb = lds + (2 + (j & 1)) * kSlot;
+          dma(v_rsrc, key0, vb, true);
+          v_phase(j);
+          __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+          // Rows past seq_len of a ragged tile are zeroed after they land, so
+          // padding never reaches P V (0 * NaN would).
+          if (key0 + kTile > a.seq_len) {
 #pragma unroll
-    for (int kc = 0; kc < 8; kc++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) pb[kc][e] = (__bf16)sacc[kc >> 1][8 * (kc & 1) + e];
-#pragma unroll
-    for (int db = 0; db < 4; db++) {
-      const uint16_t* vrow = vt + (32 * db + li) * kVStride + 4 * hh;
-#pragma unroll
-      for (int kc = 0; kc < 8; kc++) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 16 * kc);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16 * kc + 8);
-        const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
-        const bf16x8 va = __builtin_bit_cast(bf16x8, w);
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kc], oacc[db], 0, 0, 0);
+            for (int i = 0; i < 8; i++) {
+              const int row = dma_row + 4 * i;
+              if (key0 + row >= a.seq_len)
+                *reinterpret_cast<u32x4*>(vb + row * kD + (lane & 15) * 8) = u32x4{0u, 0u, 0u, 0u};
+            }
+          }
+        }
+        __syncthreads();
+      }
+    } else {
+      for (int j = 0; j <= n; j++) {
+        if (j + 1 < n) dma(k_rsrc, cols[j + 1] * kTile, lds + ((j + 1) & 1) * kSlot, false);
+        if (j >= 1) v_phase(j - 1);                       // phase 2j
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        m_phase(j);                                       // phase 2j + 1
+        __syncthreads();
       }
     }
   }
 
+  // Merge the two key halves of each query (exact: rescale both to the larger
+  // m). Waves 4-7 leave (O, m, l) in LDS: O in the two K slots, m and l in
+  // the first V slot.
+  const float lt = l + __shfl_xor(l, 32);
+  float* xo = reinterpret_cast<float*>(lds) + qg * 64 * 64;
+  float* xm = reinterpret_cast<float*>(lds + 2 * kSlot);
+  float* xl = xm + 4 * 64;
+  if (half == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) xo[(db * 16 + r) * 64 + lane] = oacc[db][r];
+    xm[qg * 64 + lane] = m;
+    xl[qg * 64 + lane] = lt;
+  }
+  __syncthreads();
+  if (half == 1) return;
+  const float m1 = xm[qg * 64 + lane], l1 = xl[qg * 64 + lane];
+  const float mmax = fmaxf(m, m1);
+  const float f0 = __builtin_amdgcn_exp2f(m - mmax), f1 = __builtin_amdgcn_exp2f(m1 - mmax);
+  const float inv = 1.0f / fmaxf(lt * f0 + l1 * f1, 1.0e-30f);
+  const float s0 = f0 * inv, s1 = f1 * inv;
+
   // O^T C layout: lane (li, hh) holds query q0 + li, channels
   // 32db + 8g + 4hh + [0, 4) in registers 4g .. 4g + 3.
-  const float lt = l + __shfl_xor(l, 32);
-  const float inv = 1.0f / fmaxf(lt, 1.0e-30f);
   const int qi = q0 + li;
   const bool valid = qi < a.seq_len;
   uint16_t* orow = a.out_layout == H3HIP_OUT_HEAD_MAJOR
@@ -198,13 +332,19 @@ __global__ __launch_bounds__(256, 2) void bsattn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int db = 0; db < 4; db++)
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
+    for (int gg = 0; gg < 4; gg++) {
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int r = 4 * gg + e;
+        o[e] = oacc[db][r] * s0 + xo[(db * 16 + r) * 64 + lane] * s1;
+      }
       u32x2 w = {0u, 0u};
       if (valid) {
-        w[0] = pack_bf16x2(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv);
-        w[1] = pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
+        w[0] = pack_bf16x2(o[0], o[1]);
+        w[1] = pack_bf16x2(o[2], o[3]);
       }
-      *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * g + 4 * hh) = w;
+      *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * gg + 4 * hh) = w;
     }
 }
 
@@ -216,7 +356,7 @@ static int launch_bsattn(h3hip_plan p, const void* q, const void* k, const void*
                 out_layout, scale * 1.4426950408889634f};
   const unsigned grid = (unsigned)p->work.size();
   if (grid == 0) return H3HIP_OK;
-  bsattn_fwd_kernel<<<grid, 256, 0, stream>>>(args);
+  bsattn_fwd_kernel<<<grid, kThreads, 0, stream>>>(args);
   return check_launch("bsattn_fwd_kernel");
 }
 
