@@ -204,9 +204,11 @@ def main() -> int:
         ev[i][2].record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    pro_ms = float(np.median([e[0].elapsed_time(e[1]) for e in ev]))
-    attn_ms = float(np.median([e[1].elapsed_time(e[2]) for e in ev]))
-    attn_mean_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+    # Per-launch durations from events on the stream the kernels run on
+    # (torch's current stream); the roofline uses the average launch.
+    pro_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
+    attn_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+    attn_median_ms = float(np.median([e[1].elapsed_time(e[2]) for e in ev]))
     ms_per_step = wall_ms / args.steps
     attn_tflops = attn_flops / (attn_ms * 1e-3) / 1e12
     pro_bytes = 3 * S * inner * 2 + 3 * S_pad * inner * 2 + S * 12 + 2 * D * 2
@@ -236,7 +238,8 @@ def main() -> int:
             "step": "prologue(Q,K norm+RoPE, V relayout) + block-sparse attention (token-major out)",
         },
         "attn_ms": round(attn_ms, 4),
-        "attn_ms_mean": round(attn_mean_ms, 4),
+        "attn_ms_median": round(attn_median_ms, 4),
+        "attn_tflop_per_launch": round(attn_flops / 1e12, 4),
         "attn_tflops_active": round(attn_tflops, 3),
         "attn_mfma_peak_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
         "prologue_qkv_ms": round(pro_ms, 4),
@@ -271,7 +274,7 @@ def main() -> int:
                              seq_pad=S_pad, out=(qh, kh, None))
             b.record()
         torch.cuda.synchronize()
-        p5 = float(np.median([a.elapsed_time(b) for a, b in evs[3:]]))
+        p5 = float(np.mean([a.elapsed_time(b) for a, b in evs[3:]]))
         b5 = 2 * S * inner * 2 + 2 * S_pad * inner * 2 + S * 12 + 2 * D * 2
         extras["cfg5_prologue_qk"] = {
             "ms": round(p5, 4), "bytes": b5, "gbps": round(b5 / (p5 * 1e-3) / 1e9, 1),
@@ -292,7 +295,7 @@ def main() -> int:
                 ops.bsattn_fwd(p, qq, kk, vv, scale)
                 b.record()
             torch.cuda.synchronize()
-            ms = float(np.median([a.elapsed_time(b) for a, b in evs[2:]]))
+            ms = float(np.mean([a.elapsed_time(b) for a, b in evs[2:]]))
             fl = p.nnz * sh.heads * FLOP_PER_TILE_HEAD
             extras[name] = {"attn_ms": round(ms, 4), "active_tiles_per_head": p.nnz,
                             "density": round(p.density, 5),
