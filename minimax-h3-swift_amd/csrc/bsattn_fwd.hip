@@ -42,6 +42,9 @@ constexpr int kWaitVmcnt0 = 0x0F70;
 // Buffer resource word 3 for raw (untyped, unswizzled) buffer loads on gfx9:
 // DATA_FORMAT = 32 bits, everything else zero.
 constexpr int kBufferWord3 = 0x00020000;
+// Instruction classes for __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
 
 struct AttnArgs {
   const uint16_t* __restrict__ q;
@@ -196,6 +199,14 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
           sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[s], sacc[b], 0, 0, 0);
         }
       }
+      // Operand reads run four MFMAs ahead of their use.
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+#pragma unroll
+      for (int i = 0; i < 12; i++) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
     }
     if (j >= 1) {
       const uint16_t* vb = lds + (2 + ((j - 1) & 1)) * kSlot;
@@ -207,6 +218,14 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
                                        vb + v_off[1][db] + 16 * kc * kD);
           oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kc], oacc[db], 0, 0, 0);
         }
+      // Each V^T operand is two transpose reads; keep four operands in flight.
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+#pragma unroll
+      for (int i = 0; i < 12; i++) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
     }
   };
 
