@@ -82,6 +82,13 @@ __device__ __forceinline__ bf16x8 vt_operand(const uint16_t* p0, const uint16_t*
   return __builtin_bit_cast(bf16x8, w);
 }
 
+// max(x[i], x[i ^ 32]) in every lane, without going through LDS.
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& s, int base) {
   typedef float f32x8 __attribute__((ext_vector_type(8)));
   const f32x8 v = {s[base], s[base + 1], s[base + 2], s[base + 3],
@@ -246,7 +253,7 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
     for (int b = 0; b < 2; b++)
 #pragma unroll
       for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[b][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = max_xor32(mx);
     const float m_cand = fmaxf(m, mx * c);
     const bool raise = m_cand > m + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(raise) != 0) {
