@@ -200,70 +200,83 @@ __global__ __launch_bounds__(256, 5) void qk_norm_rope_kernel(PrologueArgs a) {
     unpack8(load16(gsrc + off_b), gam + 8);
   }
 
-  const int rows = kTok * a.heads;
+  // A row group keeps one token (kGroupsPerTensor is a multiple of kTok) and
+  // steps through the heads kGroupsPerTensor / kTok at a time, so both row
+  // pointers advance by constants.
+  static_assert(kGroupsPerTensor % kTok == 0 && kRowGroups % kTok == 0, "row groups vs tokens");
+  constexpr int kHeadStep = kGroupsPerTensor / kTok;
+  const int tok = g0 % kTok;
+  const int32_t s = s0 + tok;
+  const bool tok_valid = s < a.seq_len;
+  int head = g0 / kTok;
+  const uint16_t* src = in + (int64_t)s * a.ld_in + (int64_t)head * kHeadDim;
+  uint16_t* dst = out + ((int64_t)head * a.seq_pad + s) * kHeadDim;
+  const int64_t dst_step = (int64_t)kHeadStep * a.seq_pad * kHeadDim;
   const u32x4 zero = {0u, 0u, 0u, 0u};
-  auto src_of = [&](int rho) {
-    const int head = rho / kTok, tok = rho - head * kTok;
-    return (int64_t)(s0 + tok) * a.ld_in + (int64_t)head * kHeadDim;
-  };
-  auto valid = [&](int rho) { return rho < rows && s0 + (rho % kTok) < a.seq_len; };
   u32x4 na = zero, nb = zero;
-  if (valid(g0)) {
-    na = stream_load16(in + src_of(g0) + off_a);
-    nb = stream_load16(in + src_of(g0) + off_b);
+  if (tok_valid && head < a.heads) {
+    na = stream_load16(src + off_a);
+    nb = stream_load16(src + off_b);
   }
   // The first row is in flight while the rotation table is computed.
   for (int t = tid; t < kTok * half; t += 256) {
-    const int tok = t / half, p = t - tok * half;
-    const int32_t s = s0 + tok;
+    const int tk = t / half, p = t - tk * half;
+    const int32_t st = s0 + tk;
     float c = 1.f, sn = 0.f;
-    if (s < a.seq_len) {
+    if (st < a.seq_len) {
       const int axis = min(max(a.pair_axis[p], 0), 2);  // a bad table cannot index past pos
-      const float ang = a.pos[(int64_t)s * 3 + axis] * a.pair_inv[p];
+      const float ang = a.pos[(int64_t)st * 3 + axis] * a.pair_inv[p];
       sincosf(ang, &sn, &c);
     }
     if (kMode == H3HIP_ROUND_REFERENCE) {
       c = round_bf16(c);
       sn = round_bf16(sn);
     }
-    tab_lds[tok][p] = RopeEntry{c, sn};
+    tab_lds[tk][p] = RopeEntry{c, sn};
   }
 
   __syncthreads();
 
-  for (int rho = g0; rho < rows; rho += kGroupsPerTensor) {
+  const RopeEntry* tab = &tab_lds[tok][pair0];
+  for (; head < a.heads; head += kHeadStep) {
     const u32x4 ca = na, cb = nb;
-    const int next = rho + kGroupsPerTensor;
-    if (valid(next)) {
-      na = stream_load16(in + src_of(next) + off_a);
-      nb = stream_load16(in + src_of(next) + off_b);
+    src += kHeadStep * kHeadDim;
+    if (tok_valid && head + kHeadStep < a.heads) {
+      na = stream_load16(src + off_a);
+      nb = stream_load16(src + off_b);
     }
-    const int head = rho / kTok, tok = rho - head * kTok;
-    const int32_t s = s0 + tok;
-    uint16_t* dst = out + ((int64_t)head * a.seq_pad + s) * kHeadDim;
     u32x4 oa = zero, ob = zero;
-    if (s < a.seq_len) {
+    if (tok_valid) {
       float x[16];
       unpack8(ca, x);
       unpack8(cb, x + 8);
-      norm_rope<kMode, kFull>(x, gam, pair_lane, &tab_lds[tok][pair0], a.eps, oa, ob);
+      norm_rope<kMode, kFull>(x, gam, pair_lane, tab, a.eps, oa, ob);
     }
     store16(dst + off_a, oa);
     store16(dst + off_b, ob);
+    dst += dst_step;
   }
 
   if (a.v_in) {
-    for (int rho = grp; rho < rows; rho += kRowGroups) {
-      const int head = rho / kTok, tok = rho - head * kTok;
-      const int32_t s = s0 + tok;
-      uint16_t* dst = a.v_out + ((int64_t)head * a.seq_pad + s) * kHeadDim;
+    // V rows: all row groups, token grp % kTok, heads kRowGroups / kTok apart.
+    constexpr int kVStep = kRowGroups / kTok;
+    const int vtok = grp % kTok;
+    const int32_t vs = s0 + vtok;
+    const bool v_valid = vs < a.seq_len;
+    int vh = grp / kTok;
+    const uint16_t* vsrc = a.v_in + (int64_t)vs * a.ld_in + (int64_t)vh * kHeadDim;
+    uint16_t* vdst = a.v_out + ((int64_t)vh * a.seq_pad + vs) * kHeadDim;
+    const int64_t vdst_step = (int64_t)kVStep * a.seq_pad * kHeadDim;
+    for (; vh < a.heads; vh += kVStep) {
       u32x4 va = zero, vb = zero;
-      if (s < a.seq_len) {
-        va = stream_load16(a.v_in + src_of(rho) + off_a);
-        vb = stream_load16(a.v_in + src_of(rho) + off_b);
+      if (v_valid) {
+        va = stream_load16(vsrc + off_a);
+        vb = stream_load16(vsrc + off_b);
       }
-      store16(dst + off_a, va);
-      store16(dst + off_b, vb);
+      store16(vdst + off_a, va);
+      store16(vdst + off_b, vb);
+      vsrc += kVStep * kHeadDim;
+      vdst += vdst_step;
     }
   }
 }
