@@ -282,7 +282,8 @@ def main() -> int:
             "traffic": read_traffic("qk_norm_rope_cfg5_traffic.txt"),
         }
         del q_in, k_in
-        for name in ("cfg3_1344x768x5s_frame0", "cfg2_864x480x7s", "cfg4_dense_864x480x7s"):
+        for name in ("cfg3_1344x768x5s_frame0", "cfg2_864x480x7s", "cfg4_dense_864x480x7s",
+                     "axial_h3_864x480x124"):
             sh = C.ALL[name]
             p = h3hip.TilePlan(sh.mask_rule(), heads=sh.heads)
             qq = torch.randn((sh.heads, p.seq_pad, D), generator=g, device=dev).to(torch.bfloat16)
@@ -301,6 +302,11 @@ def main() -> int:
                             "density": round(p.density, 5),
                             "tflops_active": round(fl / (ms * 1e-3) / 1e12, 3),
                             "mfma_peak_frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+            if sh.rule == "axial":
+                kw = sh.oracle_rule_kwargs()
+                extras[name]["heads"] = sh.heads
+                extras[name]["token_density"] = round(h3hip.axial_token_density(
+                    sh.prefix_len, sh.frames, sh.height, sh.width, kw["landmarks"]), 5)
             del qq, kk, vv
             p.close()
         result["extras"] = extras

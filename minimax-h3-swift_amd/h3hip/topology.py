@@ -96,6 +96,24 @@ def landmark_frames(frames: int, n: int = 3) -> list[int]:
     return [int(v) for v in out[:cnt]]
 
 
+def axial_token_density(prefix_len: int, frames: int, height: int, width: int,
+                        landmarks) -> float:
+    """Token-level density of the axial topology, AxialTopology.density
+    (Sources/H3Attention/AxialTopology.swift:139-170): prefix rows see all S
+    keys; a video query in frame f sees the prefix, every token of frame f
+    and of each landmark frame, and one token (its own position) in every
+    other frame -- counted frame by frame, so the overlapping axes are never
+    added twice."""
+    per = height * width
+    s = prefix_len + frames * per
+    lm = set(int(f) for f in landmarks)
+    video = 0
+    for f0 in range(frames):
+        full = len(lm) if f0 in lm else len(lm) + 1
+        video += per * (prefix_len + per * full + (frames - full))
+    return (prefix_len * s + video) / float(s * s)
+
+
 @dataclass
 class Policy:
     """When the backend declines (AttentionContext-driven, AttentionBackend.swift:10-59)."""
