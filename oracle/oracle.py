@@ -143,6 +143,39 @@ def randn_bf16(shape, seed: int, scale: float = 1.0) -> np.ndarray:
     return f32_to_bf16(g.standard_normal(shape, dtype=np.float32) * np.float32(scale))
 
 
+_SM_GAMMA = np.uint64(0x9E3779B97F4A7C15)
+_SM_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_SM_M2 = np.uint64(0x94D049BB133111EB)
+
+
+def splitmix64(seed: int, count: int) -> np.ndarray:
+    """The splitmix64 stream (Steele, Lea and Flood, "Fast splittable
+    pseudorandom number generators", OOPSLA 2014): state_i = seed + (i+1)*gamma,
+    each mixed by two xor-shift-multiply rounds. Integer arithmetic only."""
+    with np.errstate(over="ignore"):
+        x = np.uint64(seed) + (np.arange(1, count + 1, dtype=np.uint64) * _SM_GAMMA)
+        x = (x ^ (x >> np.uint64(30))) * _SM_M1
+        x = (x ^ (x >> np.uint64(27))) * _SM_M2
+        return x ^ (x >> np.uint64(31))
+
+
+def splitmix_uniform(shape, seed: int) -> np.ndarray:
+    """Uniform [0, 1) doubles from the top 53 bits of splitmix64 draws."""
+    n = int(np.prod(shape))
+    return ((splitmix64(seed, n) >> np.uint64(11)).astype(np.float64) * 2.0 ** -53).reshape(shape)
+
+
+def splitmix_normal_bf16(shape, seed: int) -> np.ndarray:
+    """Bit-stable approximately N(0, 1) bf16 inputs: the Irwin-Hall sum of four
+    splitmix64 uniforms, centred and scaled by sqrt(3) to unit variance, rounded
+    to bf16. Every step is exact or IEEE-deterministic, so a fixture needs only
+    the seed on any machine or numpy version."""
+    n = int(np.prod(shape))
+    u = (splitmix64(seed, 4 * n) >> np.uint64(11)).astype(np.float64) * 2.0 ** -53
+    x = (u.reshape(n, 4).sum(axis=1) - 2.0) * np.sqrt(3.0)
+    return f32_to_bf16(x.astype(np.float32)).reshape(shape)
+
+
 def uniform_bf16(shape, seed: int, lo: float, hi: float) -> np.ndarray:
     g = np.random.default_rng(seed)
     return f32_to_bf16(g.uniform(lo, hi, size=shape).astype(np.float32))
@@ -267,6 +300,8 @@ def qk_norm_rope(x: np.ndarray, ld: int, S: int, S_pad: int, H: int, D: int,
     """H3RMSNorm -> SplitHalfRoPE, token-major bf16 in (row stride ``ld``),
     head-major bf16 [H, S_pad, D] out (uint16 bit patterns)."""
     x = np.ascontiguousarray(x, dtype=np.uint16)
+    if (x.ndim == 2 and x.shape[1] != ld) or x.size < (S - 1) * ld + H * D:
+        raise ValueError(f"x of shape {x.shape} does not hold {S} rows of stride {ld}")
     gamma = np.ascontiguousarray(gamma, dtype=np.uint16)
     pos = np.ascontiguousarray(pos, dtype=np.float32)
     pair_axis = np.ascontiguousarray(pair_axis, dtype=np.int32)

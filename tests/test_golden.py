@@ -1,5 +1,7 @@
-"""The committed tile-list fixtures are what the oracle's brute force gives,
-and carry the counts the rules are documented with."""
+"""The committed fixtures: tile lists are what the oracle's brute force gives
+and carry the counts the rules are documented with; the attention and
+prologue output vectors are what the oracle computes from their seeded,
+bit-stable inputs (so a change to the oracle that moves them is caught)."""
 import glob
 import os
 import sys
@@ -29,6 +31,32 @@ def load(name):
 def test_fixture_set_is_complete():
     names = sorted(os.path.basename(p)[6:-4] for p in glob.glob(os.path.join(HERE, "golden", "tiles_*.npz")))
     assert names == sorted(EXPECTED_NNZ)
+    for f in ("attn_h2_s600.npz", "prologue_h2_s300.npz"):
+        assert os.path.exists(os.path.join(HERE, "golden", f))
+
+
+def test_splitmix64_known_answer(orc):
+    """splitmix64's published first outputs for seed 0."""
+    got = [int(x) for x in orc.splitmix64(0, 3)]
+    assert got == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+    x = orc.bf16_to_f32(orc.splitmix_normal_bf16((200000,), 3))
+    assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1.0) < 0.01
+    assert float(np.abs(x).max()) <= 2.0 * np.sqrt(3.0)
+
+
+def test_attention_golden_is_what_the_oracle_computes(orc):
+    z = np.load(os.path.join(HERE, "golden", "attn_h2_s600.npz"))
+    assert np.array_equal(z["bitmap"], make_golden.attn_bitmap())
+    want = orc.bf16_to_f32(z["out_bf16"])
+    got = make_golden.attn_expected()
+    assert np.all(got[:, 256:384] == 0)                      # the empty tile row
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -8 + 1e-7)
+
+
+def test_prologue_golden_is_bit_identical(orc):
+    z = np.load(os.path.join(HERE, "golden", "prologue_h2_s300.npz"))
+    q, k = make_golden.prologue_expected()
+    assert np.array_equal(q, z["q"]) and np.array_equal(k, z["k"])
 
 
 @pytest.mark.parametrize("name,kw", list(make_golden.rules()))
