@@ -188,6 +188,28 @@ int h3hip_qk_norm_rope(const void* q_in, const void* k_in, int64_t ld_in, const 
 int h3hip_bsattn_fwd(h3hip_plan plan, const void* q, const void* k, const void* v, int32_t heads,
                      int32_t head_dim, float scale, void* out, int32_t out_layout, void* stream);
 
+/* A [heads, rows, head_dim] bf16 view of a caller tensor: element (h, s, d)
+ * at data + h*head_stride + s*row_stride + d (strides in elements, multiples
+ * of 8; row_stride >= head_dim). A head-major buffer is {seq_pad*128, 128};
+ * V straight out of a fused token-major Q|K|V projection is
+ * {128, 3*heads*128} at qkv + 2*heads*128. */
+typedef struct {
+  void* data;
+  int64_t head_stride;
+  int64_t row_stride;
+} h3hip_view;
+
+/* h3hip_bsattn_fwd on strided views, the arrays SDPABackend.attend receives
+ * (AttentionBackend.swift:141-154): AttentionLayer hands it lazily transposed
+ * [B, H, S, D] views of the projection (DiTBlock.swift:323-327, 346-352), so
+ * V needs no copy. Reads rows < seq_len of q, k, v only (no padding rows
+ * need exist) and writes rows < seq_len of out; rows with no active tile are
+ * zero. K and V rows are fetched with 32-bit offsets: seq_pad * row_stride * 2
+ * must stay below 2^31. Same declines as h3hip_bsattn_fwd. */
+int h3hip_bsattn_fwd_strided(h3hip_plan plan, const h3hip_view* q, const h3hip_view* k,
+                             const h3hip_view* v, int32_t heads, int32_t head_dim, float scale,
+                             const h3hip_view* out, void* stream);
+
 /* H3AttentionBackend.attend (AttentionBackend.swift:123-127) with its context:
  * applies the plan's policy and geometry checks, then runs h3hip_bsattn_fwd
  * with a head-major output. H3HIP_DECLINED = the caller runs dense. */

@@ -46,6 +46,9 @@ constexpr int kBufferWord3 = 0x00020000;
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 
+// Each tensor is a [heads, rows, 128] view: element (h, s, d) at
+// base + h*head_stride + s*row_stride + d. Only rows < seq_len of q, k and v
+// are read; rows < out_rows of out are written (zero past seq_len).
 struct AttnArgs {
   const uint16_t* __restrict__ q;
   const uint16_t* __restrict__ k;
@@ -54,7 +57,9 @@ struct AttnArgs {
   const int32_t* __restrict__ row_ptr;
   const int32_t* __restrict__ col_idx;
   const int32_t* __restrict__ work;
-  int32_t seq_len, seq_pad, heads, out_layout;
+  int64_t q_hs, k_hs, v_hs, o_hs;  // head strides (elements)
+  int32_t q_rs, k_rs, v_rs, o_rs;  // row strides (elements)
+  int32_t seq_len, out_rows;
   float scale_log2;
 };
 
@@ -123,17 +128,21 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
   const int qg = wave & 3, half = wave >> 2;
   const int li = lane & 31, hh = lane >> 5;
-  const size_t head_off = (size_t)head * a.seq_pad * kD;
-  const uint16_t* qh = a.q + head_off;
   const int q0 = qt * kTile + qg * 32;
   const float c = a.scale_log2;
 
-  // Q^T as the B operand: lane (li, hh) holds Q[q0 + li][16s + 8hh .. +7].
+  // Q^T as the B operand: lane (li, hh) holds Q[q0 + li][16s + 8hh .. +7];
+  // query rows past seq_len are not read (zero).
   bf16x8 qreg[8];
   {
-    const uint16_t* qrow = qh + (size_t)(q0 + li) * kD + 8 * hh;
+    const bool q_valid = q0 + li < a.seq_len;
+    const uint16_t* qrow =
+        a.q + head * a.q_hs + (int64_t)(q_valid ? q0 + li : 0) * a.q_rs + 8 * hh;
 #pragma unroll
-    for (int s = 0; s < 8; s++) qreg[s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
+    for (int s = 0; s < 8; s++) {
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
+      qreg[s] = q_valid ? x : bf16x8{};
+    }
   }
 
   // K operand offsets: block b row half*64 + 32b + li, chunk 2s + hh.
@@ -154,25 +163,27 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
     }
 
   // HBM -> LDS by one half of the workgroup, as buffer loads (a per-head
-  // resource, the key offset in an SGPR, 32-bit lane offsets): wave w moves
-  // rows 32(w&3) .. +31 of a tile, 4 rows per instruction; lane l fills chunk
+  // resource bounded at row seq_len, 32-bit lane offsets): wave w moves rows
+  // 32(w&3) .. +31 of a tile, 4 rows per instruction; lane l fills chunk
   // position l%16 of row 32(w&3) + 4i + l/16 from the global chunk that the
-  // swizzle places there.
-  const int head_bytes = a.seq_pad * kD * 2;
-  const __amdgpu_buffer_rsrc_t k_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(a.k + head_off), 0, head_bytes, kBufferWord3);
-  const __amdgpu_buffer_rsrc_t v_rsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(a.v + head_off), 0, head_bytes, kBufferWord3);
+  // swizzle places there. The whole offset is in the lane offset, which the
+  // hardware range-checks, so rows at or past seq_len are never fetched.
+  const int k_rs2 = a.k_rs * 2, v_rs2 = a.v_rs * 2;
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.k + head * a.k_hs), 0, (a.seq_len - 1) * k_rs2 + kD * 2, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.v + head * a.v_hs), 0, (a.seq_len - 1) * v_rs2 + kD * 2, kBufferWord3);
   const int dma_row = 32 * qg + (lane >> 4);
   auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int key0, uint16_t* slot,
                  bool v_layout) __attribute__((always_inline)) {
+    const int rs2 = v_layout ? v_rs2 : k_rs2;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const int row = dma_row + 4 * i;
       const int swz = v_layout ? v_swz(row) : k_swz(row);
-      const int voff = row * (kD * 2) + (((lane & 15) ^ swz) * 16);
+      const int voff = (key0 + row) * rs2 + (((lane & 15) ^ swz) * 16);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsrc, (lds_void*)(slot + (32 * qg + 4 * i) * kD), 16, voff, key0 * (kD * 2), 0, 0);
+          rsrc, (lds_void*)(slot + (32 * qg + 4 * i) * kD), 16, voff, 0, 0, 0);
     }
   };
 
@@ -352,9 +363,8 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
   // 32db + 8g + 4hh + [0, 4) in registers 4g .. 4g + 3.
   const int qi = q0 + li;
   const bool valid = qi < a.seq_len;
-  uint16_t* orow = a.out_layout == H3HIP_OUT_HEAD_MAJOR
-                       ? a.out + head_off + (size_t)qi * kD
-                       : a.out + (size_t)qi * a.heads * kD + (size_t)head * kD;
+  if (qi >= a.out_rows) return;
+  uint16_t* orow = a.out + head * a.o_hs + (int64_t)qi * a.o_rs;
 #pragma unroll
   for (int db = 0; db < 4; db++)
 #pragma unroll
@@ -374,16 +384,48 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
     }
 }
 
-static int launch_bsattn(h3hip_plan p, const void* q, const void* k, const void* v,
-                         float scale, void* out, int32_t out_layout, hipStream_t stream) {
-  AttnArgs args{static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out),
-                p->d_row_ptr, p->d_col_idx, p->d_work, p->seq_len, p->seq_pad, p->heads,
-                out_layout, scale * 1.4426950408889634f};
+// One [heads, rows, 128] view of a caller tensor (strides in elements).
+struct View {
+  const void* ptr;
+  int64_t head_stride, row_stride;
+};
+
+static int launch_bsattn(h3hip_plan p, const View& q, const View& k, const View& v,
+                         const View& o, int32_t out_rows, float scale, hipStream_t stream) {
+  AttnArgs args{static_cast<const uint16_t*>(q.ptr),
+                static_cast<const uint16_t*>(k.ptr),
+                static_cast<const uint16_t*>(v.ptr),
+                static_cast<uint16_t*>(const_cast<void*>(o.ptr)),
+                p->d_row_ptr,
+                p->d_col_idx,
+                p->d_work,
+                q.head_stride,
+                k.head_stride,
+                v.head_stride,
+                o.head_stride,
+                (int32_t)q.row_stride,
+                (int32_t)k.row_stride,
+                (int32_t)v.row_stride,
+                (int32_t)o.row_stride,
+                p->seq_len,
+                out_rows,
+                scale * 1.4426950408889634f};
   const unsigned grid = (unsigned)p->work.size();
   if (grid == 0) return H3HIP_OK;
   bsattn_fwd_kernel<<<grid, kThreads, 0, stream>>>(args);
   return check_launch("bsattn_fwd_kernel");
+}
+
+// Checks shared by both entry points; H3HIP_OK or the code to return.
+static int check_attention_call(h3hip_plan plan, int32_t heads, int32_t head_dim, float scale) {
+  H3_REQUIRE(plan != nullptr, H3HIP_EINVAL, "plan is NULL");
+  if (head_dim != kD || heads != plan->heads) {
+    set_error("declined: head_dim %d heads %d (needs head_dim 128 and the plan's %d heads)",
+              head_dim, heads, plan->heads);
+    return H3HIP_DECLINED;
+  }
+  H3_REQUIRE(std::isfinite(scale) && scale > 0.f, H3HIP_EINVAL, "scale must be finite and > 0");
+  return H3HIP_OK;
 }
 
 }  // namespace h3hip
@@ -393,20 +435,50 @@ using namespace h3hip;
 extern "C" int h3hip_bsattn_fwd(h3hip_plan plan, const void* q, const void* k, const void* v,
                                 int32_t heads, int32_t head_dim, float scale, void* out,
                                 int32_t out_layout, void* stream) {
-  H3_REQUIRE(plan != nullptr, H3HIP_EINVAL, "plan is NULL");
-  if (head_dim != kD || heads != plan->heads) {
-    set_error("declined: head_dim %d heads %d (needs head_dim 128 and the plan's %d heads)",
-              head_dim, heads, plan->heads);
-    return H3HIP_DECLINED;
-  }
+  const int rc = check_attention_call(plan, heads, head_dim, scale);
+  if (rc != H3HIP_OK) return rc;
   H3_REQUIRE(q && k && v && out, H3HIP_EINVAL, "NULL tensor argument");
   auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   H3_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), H3HIP_EINVAL,
              "tensors must be 16-byte aligned");
-  H3_REQUIRE(std::isfinite(scale) && scale > 0.f, H3HIP_EINVAL, "scale must be finite and > 0");
   H3_REQUIRE(out_layout == H3HIP_OUT_HEAD_MAJOR || out_layout == H3HIP_OUT_TOKEN_MAJOR,
              H3HIP_EINVAL, "unknown out_layout %d", out_layout);
-  return launch_bsattn(plan, q, k, v, scale, out, out_layout, as_stream(stream));
+  const int64_t hm = (int64_t)plan->seq_pad * kD;
+  const View o = out_layout == H3HIP_OUT_HEAD_MAJOR
+                     ? View{out, hm, kD}
+                     : View{out, kD, (int64_t)plan->heads * kD};
+  return launch_bsattn(plan, View{q, hm, kD}, View{k, hm, kD}, View{v, hm, kD}, o,
+                       plan->seq_pad, scale, as_stream(stream));
+}
+
+extern "C" int h3hip_bsattn_fwd_strided(h3hip_plan plan, const h3hip_view* q,
+                                        const h3hip_view* k, const h3hip_view* v,
+                                        int32_t heads, int32_t head_dim, float scale,
+                                        const h3hip_view* out, void* stream) {
+  const int rc = check_attention_call(plan, heads, head_dim, scale);
+  if (rc != H3HIP_OK) return rc;
+  H3_REQUIRE(q && k && v && out, H3HIP_EINVAL, "NULL view argument");
+  const h3hip_view* views[4] = {q, k, v, out};
+  const char* names[4] = {"q", "k", "v", "out"};
+  for (int i = 0; i < 4; i++) {
+    const h3hip_view& t = *views[i];
+    H3_REQUIRE(t.data != nullptr, H3HIP_EINVAL, "%s: NULL data", names[i]);
+    H3_REQUIRE((reinterpret_cast<uintptr_t>(t.data) & 15u) == 0, H3HIP_EINVAL,
+               "%s: data must be 16-byte aligned", names[i]);
+    H3_REQUIRE(t.head_stride >= 0 && t.head_stride % 8 == 0, H3HIP_EINVAL,
+               "%s: head_stride %lld must be a non-negative multiple of 8", names[i],
+               (long long)t.head_stride);
+    H3_REQUIRE(t.row_stride >= kD && t.row_stride % 8 == 0 && t.row_stride <= INT32_MAX,
+               H3HIP_EINVAL, "%s: row_stride %lld must be a multiple of 8 and >= %d", names[i],
+               (long long)t.row_stride, kD);
+  }
+  // K and V are fetched with 32-bit offsets from each head's base.
+  for (int i = 1; i < 3; i++)
+    H3_REQUIRE((int64_t)plan->seq_pad * views[i]->row_stride * 2 < ((int64_t)1 << 31),
+               H3HIP_EINVAL, "%s: seq_pad x row_stride exceeds 32-bit offsets", names[i]);
+  auto as_view = [](const h3hip_view* t) { return View{t->data, t->head_stride, t->row_stride}; };
+  return launch_bsattn(plan, as_view(q), as_view(k), as_view(v), as_view(out), plan->seq_len,
+                       scale, as_stream(stream));
 }
 
 extern "C" int h3hip_attend(h3hip_plan plan, const h3hip_attention_context* ctx, const void* q,

@@ -68,6 +68,15 @@ class AttentionContextC(ctypes.Structure):
     ]
 
 
+class ViewC(ctypes.Structure):
+    """h3hip_view: element (h, s, d) at data + h*head_stride + s*row_stride + d."""
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("head_stride", ctypes.c_int64),
+        ("row_stride", ctypes.c_int64),
+    ]
+
+
 # Every symbol include/ch3hip.h declares, with (restype, argtypes).
 SIGNATURES = {
     "h3hip_device_supported": (ctypes.c_int, [ctypes.c_int32]),
@@ -90,6 +99,10 @@ SIGNATURES = {
                                           ctypes.c_int32, ctypes.c_int32, _vp, _vp, _vp, _vp]),
     "h3hip_bsattn_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32,
                                         ctypes.c_float, _vp, ctypes.c_int32, _vp]),
+    "h3hip_bsattn_fwd_strided": (ctypes.c_int, [_vp, ctypes.POINTER(ViewC),
+                                                ctypes.POINTER(ViewC), ctypes.POINTER(ViewC),
+                                                ctypes.c_int32, ctypes.c_int32, ctypes.c_float,
+                                                ctypes.POINTER(ViewC), _vp]),
     "h3hip_attend": (ctypes.c_int, [_vp, ctypes.POINTER(AttentionContextC), _vp, _vp, _vp,
                                     ctypes.c_int32, ctypes.c_int32, ctypes.c_float, _vp, _vp]),
     "h3hip_rope_pairs_axes": (ctypes.c_int, [ctypes.c_double, ctypes.c_int32, ctypes.c_int32,

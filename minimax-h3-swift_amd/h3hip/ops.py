@@ -157,6 +157,40 @@ def bsattn_fwd(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     return out
 
 
+def _view(name: str, t: torch.Tensor, min_rows: int) -> L.ViewC:
+    """[heads, rows, head_dim] tensor -> h3hip_view (strides in elements)."""
+    _require_gpu_bf16(name, t)
+    if t.dim() != 3 or t.stride(2) != 1 or t.shape[1] < min_rows:
+        raise ValueError(f"{name} must be a [heads, >= {min_rows}, head_dim] view with unit "
+                         f"stride along head_dim, got shape {tuple(t.shape)} strides {t.stride()}")
+    return L.ViewC(t.data_ptr(), t.stride(0), t.stride(1))
+
+
+def bsattn_fwd_strided(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       scale: float | None = None, out: torch.Tensor | None = None):
+    """Block-sparse attention on strided [heads, rows, head_dim] views.
+
+    q, k, v may be views straight into a fused token-major projection (e.g.
+    ``qkv.view(S, 3, H, D)[:, 2].transpose(0, 1)`` for V); only rows < S are
+    read. ``out`` is a [heads, >= S, head_dim] view to write rows < S into;
+    by default a token-major [S, heads*head_dim] tensor is allocated and
+    returned. Returns None when the call is declined."""
+    S = plan.seq_len
+    H, _, D = q.shape
+    ret = None
+    if out is None:
+        ret = torch.empty((S, H * D), dtype=torch.bfloat16, device=q.device)
+        out = ret.view(S, H, D).transpose(0, 1)
+    views = [_view(n, t, S) for n, t in (("q", q), ("k", k), ("v", v), ("out", out))]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    rc = L.lib().h3hip_bsattn_fwd_strided(plan.handle, ctypes.byref(views[0]),
+                                          ctypes.byref(views[1]), ctypes.byref(views[2]), H, D,
+                                          scale, ctypes.byref(views[3]), _stream(q))
+    if L.check(rc, allow_declined=True) == L.DECLINED:
+        return None
+    return ret if ret is not None else out
+
+
 def attend(plan: TilePlan, context, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
            scale: float, out: torch.Tensor | None = None):
     """h3hip_attend: policy + geometry checks, then the sparse kernel.

@@ -73,6 +73,9 @@ def test_plan_refuses_bad_rules_before_touching_a_device(h3):
     assert lib.h3hip_plan_create(ctypes.byref(c), 4, None, None, ctypes.byref(out)) == _lib.EINVAL
     assert "lattice" in h3.last_error()
     assert lib.h3hip_bsattn_fwd(None, None, None, None, 4, 128, 0.1, None, 0, None) == _lib.EINVAL
+    assert lib.h3hip_bsattn_fwd_strided(None, None, None, None, 4, 128, 0.1, None,
+                                        None) == _lib.EINVAL
+    assert "plan is NULL" in h3.last_error()
 
 
 def test_prologue_declines_unsupported_geometry(h3):
