@@ -217,6 +217,16 @@ int h3hip_attend(h3hip_plan plan, const h3hip_attention_context* ctx, const void
                  const void* k, const void* v, int32_t heads, int32_t head_dim, float scale,
                  void* out, void* stream);
 
+/* H3AttentionBackend.attend (AttentionBackend.swift:123-127) on the strided
+ * [B, H, S, D] views the backend receives from AttentionLayer.sdpa
+ * (DiTBlock.swift:293-316): the policy and geometry checks of h3hip_attend,
+ * then h3hip_bsattn_fwd_strided. No padding or copy is needed on either side;
+ * rows < seq_len of out are written. */
+int h3hip_attend_strided(h3hip_plan plan, const h3hip_attention_context* ctx,
+                         const h3hip_view* q, const h3hip_view* k, const h3hip_view* v,
+                         int32_t heads, int32_t head_dim, float scale, const h3hip_view* out,
+                         void* stream);
+
 /* ------------------------------------------------- host-side table helpers */
 
 /* Three-axis RoPE pair table: dim_t/dim_h/dim_w channels per axis in t|h|w

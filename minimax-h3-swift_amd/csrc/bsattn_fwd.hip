@@ -481,9 +481,10 @@ extern "C" int h3hip_bsattn_fwd_strided(h3hip_plan plan, const h3hip_view* q,
                        scale, as_stream(stream));
 }
 
-extern "C" int h3hip_attend(h3hip_plan plan, const h3hip_attention_context* ctx, const void* q,
-                            const void* k, const void* v, int32_t heads, int32_t head_dim,
-                            float scale, void* out, void* stream) {
+// The decline policy of H3AttentionBackend.attend (AttentionBackend.swift:123-127)
+// with its AttentionContext: H3HIP_OK to run, H3HIP_DECLINED (caller runs
+// dense) or an error.
+static int attend_policy(h3hip_plan plan, const h3hip_attention_context* ctx) {
   H3_REQUIRE(plan != nullptr, H3HIP_EINVAL, "plan is NULL");
   // No context means dense: a backend that does not know its block or its
   // schedule position cannot honour its own policy
@@ -515,6 +516,23 @@ extern "C" int h3hip_attend(h3hip_plan plan, const h3hip_attention_context* ctx,
               ctx->block_count, ctx->schedule_progress);
     return H3HIP_DECLINED;
   }
+  return H3HIP_OK;
+}
+
+extern "C" int h3hip_attend(h3hip_plan plan, const h3hip_attention_context* ctx, const void* q,
+                            const void* k, const void* v, int32_t heads, int32_t head_dim,
+                            float scale, void* out, void* stream) {
+  const int rc = attend_policy(plan, ctx);
+  if (rc != H3HIP_OK) return rc;
   return h3hip_bsattn_fwd(plan, q, k, v, heads, head_dim, scale, out, H3HIP_OUT_HEAD_MAJOR,
                           stream);
+}
+
+extern "C" int h3hip_attend_strided(h3hip_plan plan, const h3hip_attention_context* ctx,
+                                    const h3hip_view* q, const h3hip_view* k,
+                                    const h3hip_view* v, int32_t heads, int32_t head_dim,
+                                    float scale, const h3hip_view* out, void* stream) {
+  const int rc = attend_policy(plan, ctx);
+  if (rc != H3HIP_OK) return rc;
+  return h3hip_bsattn_fwd_strided(plan, q, k, v, heads, head_dim, scale, out, stream);
 }

@@ -103,6 +103,11 @@ SIGNATURES = {
                                                 ctypes.POINTER(ViewC), ctypes.POINTER(ViewC),
                                                 ctypes.c_int32, ctypes.c_int32, ctypes.c_float,
                                                 ctypes.POINTER(ViewC), _vp]),
+    "h3hip_attend_strided": (ctypes.c_int, [_vp, ctypes.POINTER(AttentionContextC),
+                                            ctypes.POINTER(ViewC), ctypes.POINTER(ViewC),
+                                            ctypes.POINTER(ViewC), ctypes.c_int32,
+                                            ctypes.c_int32, ctypes.c_float,
+                                            ctypes.POINTER(ViewC), _vp]),
     "h3hip_attend": (ctypes.c_int, [_vp, ctypes.POINTER(AttentionContextC), _vp, _vp, _vp,
                                     ctypes.c_int32, ctypes.c_int32, ctypes.c_float, _vp, _vp]),
     "h3hip_rope_pairs_axes": (ctypes.c_int, [ctypes.c_double, ctypes.c_int32, ctypes.c_int32,

@@ -111,23 +111,26 @@ class H3HIPBackend(H3AttentionBackend):
             return False
 
     def attend(self, queries, keys, values, scale, mask, context):
-        if self.plan is None or mask is not None or not queries.is_cuda:
+        """[H, S, D] bf16 views in (the transposed [S, H, D] arrays sdpa hands
+        over, used in place), [H, S, D] view of a token-major [S, H*D] buffer
+        out; None declines (another dtype, a mask, another shape, the policy)."""
+        if (self.plan is None or mask is not None or not queries.is_cuda
+                or queries.dtype != torch.bfloat16):
             return None
         from . import ops
         H, S, D = queries.shape
-        pad = self.plan.seq_pad
         if S != self.plan.seq_len:
             return None
 
-        def padded(t):
-            if S == pad:
-                return t.contiguous()
-            out = torch.zeros((H, pad, D), dtype=t.dtype, device=t.device)
-            out[:, :S] = t
-            return out
+        def in_place(t):
+            # Rows must be 16-byte aligned with unit stride along D; anything
+            # else is made contiguous first.
+            ok = (t.dtype == torch.bfloat16 and t.stride(2) == 1 and t.stride(1) >= D
+                  and t.stride(1) % 8 == 0 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0)
+            return t if ok else t.contiguous()
 
-        out = ops.attend(self.plan, context, padded(queries), padded(keys), padded(values), scale)
-        return None if out is None else out[:, :S]
+        return ops.attend_strided(self.plan, context, in_place(queries), in_place(keys),
+                                  in_place(values), scale)
 
 
 @dataclass

@@ -191,6 +191,29 @@ def bsattn_fwd_strided(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torc
     return ret if ret is not None else out
 
 
+def attend_strided(plan: TilePlan, context, q: torch.Tensor, k: torch.Tensor,
+                   v: torch.Tensor, scale: float, out: torch.Tensor | None = None):
+    """h3hip_attend_strided: policy + geometry checks, then the sparse kernel
+    on [heads, rows, head_dim] views (rows >= S; unit stride along head_dim).
+
+    ``out`` is a [heads, >= S, head_dim] view; by default a token-major
+    [S, heads*head_dim] buffer is allocated and its [heads, S, head_dim] view
+    returned. Returns None when the call is declined."""
+    S = plan.seq_len
+    H, _, D = q.shape
+    if out is None:
+        out = torch.empty((S, H * D), dtype=torch.bfloat16, device=q.device)
+        out = out.view(S, H, D).transpose(0, 1)
+    views = [_view(n, t, S) for n, t in (("q", q), ("k", k), ("v", v), ("out", out))]
+    cctx = None if context is None else ctypes.byref(context.to_c())
+    rc = L.lib().h3hip_attend_strided(plan.handle, cctx, ctypes.byref(views[0]),
+                                      ctypes.byref(views[1]), ctypes.byref(views[2]), H, D,
+                                      scale, ctypes.byref(views[3]), _stream(q))
+    if L.check(rc, allow_declined=True) == L.DECLINED:
+        return None
+    return out
+
+
 def attend(plan: TilePlan, context, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
            scale: float, out: torch.Tensor | None = None):
     """h3hip_attend: policy + geometry checks, then the sparse kernel.

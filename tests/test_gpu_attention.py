@@ -180,6 +180,34 @@ def test_attend_policy_and_context(h3):
     assert got is not None and torch.equal(got, want)
 
 
+def test_attend_strided_policy_matches_attend(h3):
+    """h3hip_attend_strided declines exactly where h3hip_attend does, and on
+    views of a token-major [S, H, D] buffer (no padding rows) answers
+    bit-identically to the head-major call."""
+    from h3hip import ops
+    from h3hip.backend import AttentionContext
+    note("attend_strided policy")
+    rule = h3.MaskRule.local_window(prefix_len=100, frames=4, height=10, width=12)
+    pol = h3.Policy(dense_first_blocks=1, dense_last_blocks=1, dense_until_progress=0.2)
+    plan = h3.TilePlan(rule, heads=2, policy=pol)
+    q, k, v = head_major_inputs(2, plan.seq_len, plan.seq_pad, 128, 6)
+    S = plan.seq_len
+    tm = [t[:, :S].transpose(0, 1).contiguous() for t in (q, k, v)]   # [S, H, D]
+    qv, kv, vv = (t.transpose(0, 1) for t in tm)                      # [H, S, D] views
+    span = range(100, S)
+    for ctx in (None, AttentionContext(0, 50, 0.5, S, span), AttentionContext(49, 50, 0.5, S, span),
+                AttentionContext(12, 50, 0.1, S, span), AttentionContext(12, 50, 0.5, S + 1, span),
+                AttentionContext(12, 50, 0.5, S, range(90, S))):
+        assert ops.attend(plan, ctx, q, k, v, 0.088) is None
+        assert ops.attend_strided(plan, ctx, qv, kv, vv, 0.088) is None
+    ok = AttentionContext(12, 50, 0.5, S, span)
+    got = ops.attend_strided(plan, ok, qv, kv, vv, 0.088)
+    want = ops.attend(plan, ok, q, k, v, 0.088)
+    torch.cuda.synchronize()
+    assert got is not None and got.shape == (2, S, 128)
+    assert torch.equal(got.contiguous(), want[:, :S])
+
+
 def test_backend_through_the_sdpa_seam(h3):
     """AttentionLayer.sdpa with the HIP backend and a context: the backend
     answers ([S, H, D] in, [S, H*D] out), within tolerance of dense when the
