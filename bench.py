@@ -30,6 +30,7 @@ METRIC = "block-sparse attn TFLOP/s (active tiles) + % MFMA peak at 31k tokens; 
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA, spec sheet
 PEAK_HBM_GBPS = 8000.0        # MI355X HBM3E, spec sheet
 FLOP_PER_TILE_HEAD = 4 * 128 ** 3   # QK^T and PV over one 128x128 tile, head_dim 128
+C_HIDDEN = 5120               # the benchmark configs' model width (input of the QKV projection)
 
 
 def read_traffic(name: str):
@@ -102,6 +103,15 @@ def profile_only(args, env) -> int:
         torch.cuda.synchronize()
         print(f"copy: {args.steps} x {src.numel() * 2} bytes read and written")
         return 0
+    if args.only == "qkv":
+        x, w = qkv_inputs(env)
+        vh = torch.empty_like(env["qh"])
+        for _ in range(args.warmup + args.steps):
+            ops.qkv_proj(x, w, env["gq"], env["gk"], env["pos"], env["ax"], env["inv"], heads=H,
+                         eps=env["C"].QK_EPS, seq_pad=S_pad, out=(env["qh"], env["kh"], vh))
+        torch.cuda.synchronize()
+        print(f"qkv: {args.steps} launches, x [{S}, {C_HIDDEN}] x W^T -> Q, K, V [{H}, {S_pad}, {D}]")
+        return 0
     if args.only == "attention":
         env["prologue"]()
         for _ in range(args.warmup + args.steps):
@@ -120,6 +130,65 @@ def profile_only(args, env) -> int:
     return 0
 
 
+def qkv_inputs(env):
+    """Config 3's projection operands: x [S, 5120] N(0,1), qkvWeight
+    [3*heads*128, 5120] N(0, 0.02^2), bf16."""
+    import torch
+    g, dev, S, inner = env["g"], env["dev"], env["S"], env["H"] * env["D"]
+    x = torch.randn((S, C_HIDDEN), generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn((3 * inner, C_HIDDEN), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    return x, w
+
+
+def qkv_projection_extra(args, env):
+    """The fused projection (GEMM + Q/K norm/RoPE + head-major relayout in one
+    kernel) against hipBLASLt's GEMM (torch.mm) followed by the prologue kernel,
+    at config 3. Both leave the layer's attention inputs ready (the unfused V
+    stays token-major in the qkv buffer, read in place)."""
+    import numpy as np
+    import torch
+    from h3hip import ops
+    H, S, S_pad, inner = env["H"], env["S"], env["S_pad"], env["H"] * env["D"]
+    x, w = qkv_inputs(env)
+    qh, kh = env["qh"], env["kh"]
+    vh = torch.empty_like(qh)
+    qkv_tmp = torch.empty((S, 3 * inner), dtype=torch.bfloat16, device=env["dev"])
+    tables = (env["gq"], env["gk"], env["pos"], env["ax"], env["inv"])
+
+    def fused():
+        r = ops.qkv_proj(x, w, *tables, heads=H, eps=env["C"].QK_EPS, seq_pad=S_pad,
+                         out=(qh, kh, vh))
+        assert r is not None
+
+    def gemm():
+        torch.mm(x, w.t(), out=qkv_tmp)
+
+    def prologue():
+        ops.qk_norm_rope(qkv_tmp[:, :inner], qkv_tmp[:, inner:2 * inner], *tables, heads=H,
+                         eps=env["C"].QK_EPS, seq_pad=S_pad, out=(qh, kh, None))
+
+    reps = max(10, args.steps)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(reps + 3)]
+    for e in ev:
+        e[0].record()
+        fused()
+        e[1].record()
+        gemm()
+        e[2].record()
+        prologue()
+        e[3].record()
+    torch.cuda.synchronize()
+    t = [float(np.mean([e[i].elapsed_time(e[i + 1]) for e in ev[3:]])) for i in range(3)]
+    flops = 2.0 * S * C_HIDDEN * 3 * inner
+    tf = lambda ms: round(flops / (ms * 1e-3) / 1e12, 1)
+    return {"fused_ms": round(t[0], 4), "fused_tflops": tf(t[0]),
+            "fused_mfma_peak_frac": round(flops / (t[0] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "hipblaslt_gemm_ms": round(t[1], 4), "hipblaslt_gemm_tflops": tf(t[1]),
+            "prologue_after_gemm_ms": round(t[2], 4),
+            "unfused_ms": round(t[1] + t[2], 4),
+            "gemm_tflop": round(flops / 1e12, 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -127,10 +196,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--only", choices=("attention", "prologue", "copy"),
+    ap.add_argument("--only", choices=("attention", "prologue", "copy", "qkv"),
                     help="profiling mode: run one kernel --steps times at config 3 (prologue: "
                          "config 5, Q and K only; copy: a plain 1 GiB device copy for counter "
-                         "calibration) and print nothing but a one-line summary")
+                         "calibration; qkv: the fused QKV projection) and print nothing but a one-line summary")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -286,6 +355,7 @@ def main() -> int:
             "traffic": read_traffic("qk_norm_rope_cfg5_traffic.txt"),
         }
         del q_in, k_in
+        extras["cfg3_qkv_proj"] = qkv_projection_extra(args, env=locals())
         for name in ("cfg3_1344x768x5s_frame0", "cfg2_864x480x7s", "cfg4_dense_864x480x7s",
                      "axial_h3_864x480x124"):
             sh = C.ALL[name]

@@ -175,6 +175,28 @@ int h3hip_qk_norm_rope(const void* q_in, const void* k_in, int64_t ld_in, const 
                        int32_t rounding, int32_t seq_len, int32_t seq_pad, int32_t heads,
                        int32_t head_dim, void* q_out, void* k_out, void* v_out, void* stream);
 
+/* The QKV projection of AttentionLayer.callAsFunction (DiTBlock.swift:336-345:
+ * qkv = x . qkvWeight^T, split into Q | K | V) with the Q/K prologue of
+ * DiTBlock.swift:346-352 (what h3hip_qk_norm_rope does) fused into the GEMM's
+ * epilogue, so the token-major qkv is never written. Q and K come out equal,
+ * bit for bit, to h3hip_qk_norm_rope applied to the bf16-rounded projection;
+ * V is the bf16 projection, head-major.
+ *   x:      device bf16 [seq_len, hidden], row stride ldx elements.
+ *   w:      device bf16 [3*heads*head_dim, hidden] (qkvWeight, Q | K | V rows),
+ *           row stride ldw elements.
+ *   q_gamma, k_gamma, eps, pos, pair_axis, pair_inv_freq, rot, rounding:
+ *           as for h3hip_qk_norm_rope. With both gammas NULL the call is the
+ *           plain GEMM: all three parts written unchanged (head-major).
+ *   q_out, k_out, v_out: device bf16 [heads, seq_pad, head_dim]; rows >= seq_len
+ *           are zeroed.
+ * Declines unless head_dim == 128, rot is 96 or 128, heads is even and hidden
+ * is a multiple of 64. */
+int h3hip_qkv_proj(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t hidden,
+                   const void* q_gamma, const void* k_gamma, float eps, const float* pos,
+                   const int32_t* pair_axis, const float* pair_inv_freq, int32_t rot,
+                   int32_t rounding, int32_t seq_len, int32_t seq_pad, int32_t heads,
+                   int32_t head_dim, void* q_out, void* k_out, void* v_out, void* stream);
+
 /* -------------------------------------------------------------- attention */
 
 /* Block-sparse attention over the plan's active tiles: for each query row,

@@ -26,6 +26,7 @@
 // (DPP half-row mirror, quad xor 2, quad xor 1); every lane ends with the same
 // bits. rsqrt is refined in double and rounded once to fp32.
 #include "common.h"
+#include "norm_rope.h"
 
 namespace h3hip {
 
@@ -76,14 +77,6 @@ __device__ __forceinline__ void unpack8(u32x4 w, float* f) {
   }
 }
 
-// Two fp32 values -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-  const f2 v = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, b2));
-}
-
 __device__ __forceinline__ u32x4 pack8(const float* f) {
   u32x4 r;
 #pragma unroll
@@ -99,21 +92,6 @@ constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
 template <int kCtrl>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
-}
-
-// Rotation table entry for one pair: (c, s), bf16-rounded for REFERENCE
-// rounding (the bf16 table of H3Transformer.swift:271-273), fp32 otherwise.
-struct RopeEntry {
-  float c, s;
-};
-
-// 1/sqrt(x) rounded to fp32: the hardware estimate refined by one Newton step
-// in double (relative error ~1e-13 before the final rounding), i.e. the
-// correctly rounded value except within ~1e-13 of an fp32 rounding midpoint.
-__device__ __forceinline__ float rsqrt_rounded(float x) {
-  const double xd = (double)x, r0 = (double)__builtin_amdgcn_rsqf(x);
-  const double e = fma(-xd * r0, r0, 1.0);
-  return (float)fma(0.5 * r0, e, r0);
 }
 
 // Mean of squares of the row (fixed fp32 order, see the file header) and the
@@ -142,29 +120,8 @@ __device__ __forceinline__ void norm_rope(const float* x, const float* g, bool p
   rms_normalise(x, g, eps, y);
   const bool rotate = kFull || pair_lane;
   float oa[8], ob[8];
-  if (kMode == H3HIP_ROUND_REFERENCE) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t ab = cvt_pk(y[i], y[8 + i]);  // bf16(y_a) | bf16(y_b)
-      const float a = bf16_lo(ab), b = bf16_hi(ab);
-      const float c = tab[i].c, sn = tab[i].s;
-      const uint32_t p1 = cvt_pk(c * a, -sn * b);
-      const uint32_t p2 = cvt_pk(sn * a, c * b);
-      const float ra = bf16_lo(p1) + bf16_hi(p1);
-      const float rb = bf16_lo(p2) + bf16_hi(p2);
-      oa[i] = rotate ? ra : a;
-      ob[i] = rotate ? rb : b;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float c = tab[i].c, sn = tab[i].s;
-      const float ra = c * y[i] - sn * y[8 + i];
-      const float rb = sn * y[i] + c * y[8 + i];
-      oa[i] = rotate ? ra : y[i];
-      ob[i] = rotate ? rb : y[8 + i];
-    }
-  }
+  for (int i = 0; i < 8; i++) rope_pair<kMode>(y[i], y[8 + i], tab[i], rotate, oa[i], ob[i]);
   out_a = pack8(oa);
   out_b = pack8(ob);
 }
@@ -222,17 +179,12 @@ __global__ __launch_bounds__(256, 5) void qk_norm_rope_kernel(PrologueArgs a) {
   for (int t = tid; t < kTok * half; t += 256) {
     const int tk = t / half, p = t - tk * half;
     const int32_t st = s0 + tk;
-    float c = 1.f, sn = 0.f;
+    RopeEntry e{1.f, 0.f};
     if (st < a.seq_len) {
       const int axis = min(max(a.pair_axis[p], 0), 2);  // a bad table cannot index past pos
-      const float ang = a.pos[(int64_t)st * 3 + axis] * a.pair_inv[p];
-      sincosf(ang, &sn, &c);
+      e = make_rope_entry<kMode>(a.pos[(int64_t)st * 3 + axis] * a.pair_inv[p]);
     }
-    if (kMode == H3HIP_ROUND_REFERENCE) {
-      c = round_bf16(c);
-      sn = round_bf16(sn);
-    }
-    tab_lds[tk][p] = RopeEntry{c, sn};
+    tab_lds[tk][p] = e;
   }
 
   __syncthreads();
