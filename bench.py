@@ -106,9 +106,10 @@ def profile_only(args, env) -> int:
     if args.only == "qkv":
         x, w = qkv_inputs(env)
         vh = torch.empty_like(env["qh"])
+        table = ops.rope_table(env["pos"], env["ax"], env["inv"])
         for _ in range(args.warmup + args.steps):
-            ops.qkv_proj(x, w, env["gq"], env["gk"], env["pos"], env["ax"], env["inv"], heads=H,
-                         eps=env["C"].QK_EPS, seq_pad=S_pad, out=(env["qh"], env["kh"], vh))
+            ops.qkv_proj(x, w, env["gq"], env["gk"], table, heads=H, eps=env["C"].QK_EPS,
+                         seq_pad=S_pad, out=(env["qh"], env["kh"], vh))
         torch.cuda.synchronize()
         print(f"qkv: {args.steps} launches, x [{S}, {C_HIDDEN}] x W^T -> Q, K, V [{H}, {S_pad}, {D}]")
         return 0
@@ -154,10 +155,12 @@ def qkv_projection_extra(args, env):
     vh = torch.empty_like(qh)
     qkv_tmp = torch.empty((S, 3 * inner), dtype=torch.bfloat16, device=env["dev"])
     tables = (env["gq"], env["gk"], env["pos"], env["ax"], env["inv"])
+    # The rotation table is built once per render (prepareRender), not per layer.
+    table = ops.rope_table(env["pos"], env["ax"], env["inv"])
 
     def fused():
-        r = ops.qkv_proj(x, w, *tables, heads=H, eps=env["C"].QK_EPS, seq_pad=S_pad,
-                         out=(qh, kh, vh))
+        r = ops.qkv_proj(x, w, env["gq"], env["gk"], table, heads=H, eps=env["C"].QK_EPS,
+                         seq_pad=S_pad, out=(qh, kh, vh))
         assert r is not None
 
     def gemm():

@@ -175,6 +175,18 @@ int h3hip_qk_norm_rope(const void* q_in, const void* k_in, int64_t ld_in, const 
                        int32_t rounding, int32_t seq_len, int32_t seq_pad, int32_t heads,
                        int32_t head_dim, void* q_out, void* k_out, void* v_out, void* stream);
 
+/* The rotation table of a render: H3RoPE.rotationTable(H3RoPE.angles(pos,
+ * inv_freq)) (Sources/H3Modules/H3Transformer.swift:62-78), which
+ * prepareRender builds once per render (:271-273) and every layer's
+ * AttentionLayer.callAsFunction(_:ropeTable:) takes (DiTBlock.swift:336).
+ *   pos, pair_axis, pair_inv_freq, rot: as for h3hip_qk_norm_rope.
+ *   table: device [seq_len, rot/2, 2, 2] holding [[c, -s], [s, c]] per token and
+ *          pair: bf16 for H3HIP_ROUND_REFERENCE (the reference's bf16 table),
+ *          fp32 for H3HIP_ROUND_FP32; 16-byte aligned.
+ * The entries are the ones h3hip_qk_norm_rope rotates with. */
+int h3hip_rope_table(const float* pos, const int32_t* pair_axis, const float* pair_inv_freq,
+                     int32_t rot, int32_t rounding, int32_t seq_len, void* table, void* stream);
+
 /* The QKV projection of AttentionLayer.callAsFunction (DiTBlock.swift:336-345:
  * qkv = x . qkvWeight^T, split into Q | K | V) with the Q/K prologue of
  * DiTBlock.swift:346-352 (what h3hip_qk_norm_rope does) fused into the GEMM's
@@ -184,18 +196,21 @@ int h3hip_qk_norm_rope(const void* q_in, const void* k_in, int64_t ld_in, const 
  *   x:      device bf16 [seq_len, hidden], row stride ldx elements.
  *   w:      device bf16 [3*heads*head_dim, hidden] (qkvWeight, Q | K | V rows),
  *           row stride ldw elements.
- *   q_gamma, k_gamma, eps, pos, pair_axis, pair_inv_freq, rot, rounding:
- *           as for h3hip_qk_norm_rope. With both gammas NULL the call is the
- *           plain GEMM: all three parts written unchanged (head-major).
+ *   q_gamma, k_gamma, eps, rot, rounding: as for h3hip_qk_norm_rope.
+ *   rope_table: the render's rotation table (the ropeTable argument), as
+ *           h3hip_rope_table writes it for this rounding mode: bf16 for
+ *           REFERENCE -- the reference's own table -- or fp32 for FP32.
+ *   With both gammas NULL the call is the plain GEMM: all three parts written
+ *   unchanged (head-major), rope_table unused.
  *   q_out, k_out, v_out: device bf16 [heads, seq_pad, head_dim]; rows >= seq_len
  *           are zeroed.
  * Declines unless head_dim == 128, rot is 96 or 128, heads is even and hidden
  * is a multiple of 64. */
 int h3hip_qkv_proj(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t hidden,
-                   const void* q_gamma, const void* k_gamma, float eps, const float* pos,
-                   const int32_t* pair_axis, const float* pair_inv_freq, int32_t rot,
-                   int32_t rounding, int32_t seq_len, int32_t seq_pad, int32_t heads,
-                   int32_t head_dim, void* q_out, void* k_out, void* v_out, void* stream);
+                   const void* q_gamma, const void* k_gamma, float eps, const void* rope_table,
+                   int32_t rot, int32_t rounding, int32_t seq_len, int32_t seq_pad,
+                   int32_t heads, int32_t head_dim, void* q_out, void* k_out, void* v_out,
+                   void* stream);
 
 /* -------------------------------------------------------------- attention */
 

@@ -133,17 +133,43 @@ def qk_norm_rope(q_in: torch.Tensor, k_in: torch.Tensor, q_gamma: torch.Tensor,
     return q_out, k_out, v_out
 
 
+def rope_table(pos: torch.Tensor, pair_axis: torch.Tensor, pair_inv: torch.Tensor, *,
+               rot: int | None = None, rounding: int = L.ROUND_REFERENCE,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """The render's rotation table (H3RoPE.rotationTable): [S, rot/2, 2, 2]
+    holding [[c, -s], [s, c]], bf16 for REFERENCE rounding, fp32 for FP32."""
+    for name, t, dt in (("pos", pos, torch.float32), ("pair_axis", pair_axis, torch.int32),
+                        ("pair_inv", pair_inv, torch.float32)):
+        if not t.is_cuda or t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {dt} GPU tensor")
+    rot = rot if rot is not None else 2 * pair_axis.numel()
+    if pos.dim() != 2 or pos.shape[1] != 3:
+        raise ValueError("pos must be [S, 3]")
+    if pair_axis.numel() < rot // 2 or pair_inv.numel() < rot // 2:
+        raise ValueError(f"pair tables must hold rot/2 = {rot // 2} entries")
+    S = pos.shape[0]
+    dt = torch.bfloat16 if rounding == L.ROUND_REFERENCE else torch.float32
+    shape = (S, rot // 2, 2, 2)
+    if out is None:
+        out = torch.empty(shape, dtype=dt, device=pos.device)
+    elif out.shape != shape or out.dtype != dt or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous {dt} tensor of shape {shape}")
+    L.check(L.lib().h3hip_rope_table(_ptr(pos), _ptr(pair_axis), _ptr(pair_inv), rot, rounding,
+                                     S, _ptr(out), _stream(pos)))
+    return out
+
+
 def qkv_proj(x: torch.Tensor, w: torch.Tensor, q_gamma: torch.Tensor | None = None,
-             k_gamma: torch.Tensor | None = None, pos: torch.Tensor | None = None,
-             pair_axis: torch.Tensor | None = None, pair_inv: torch.Tensor | None = None, *,
-             heads: int, head_dim: int = 128, eps: float = 1e-6, rot: int | None = None,
+             k_gamma: torch.Tensor | None = None, table: torch.Tensor | None = None, *,
+             heads: int, head_dim: int = 128, eps: float = 1e-6,
              seq_pad: int | None = None, rounding: int = L.ROUND_REFERENCE, out=None):
     """QKV projection x . w^T with the Q/K norm + RoPE prologue in its epilogue.
 
     x: [S, hidden] bf16 (row stride free, unit column stride); w: [3*heads*head_dim,
-    hidden] bf16 (Q | K | V rows). With q_gamma = k_gamma = None this is the plain
-    GEMM written head-major. Returns (q, k, v) as [heads, seq_pad, head_dim] bf16,
-    or None when the geometry is declined."""
+    hidden] bf16 (Q | K | V rows); table: the render's rotation table from
+    rope_table() for the same rounding mode ([>= S, rot/2, 2, 2]). With q_gamma =
+    k_gamma = None this is the plain GEMM written head-major. Returns (q, k, v)
+    as [heads, seq_pad, head_dim] bf16, or None when the geometry is declined."""
     _require_gpu_bf16("x", x)
     _require_gpu_bf16("w", w)
     if x.dim() != 2 or w.dim() != 2 or x.stride(1) != 1 or w.stride(1) != 1:
@@ -154,19 +180,16 @@ def qkv_proj(x: torch.Tensor, w: torch.Tensor, q_gamma: torch.Tensor | None = No
     seq_pad = seq_pad or ((S + L.TILE - 1) // L.TILE) * L.TILE
     plain = q_gamma is None and k_gamma is None
     if plain:
-        rot = head_dim if rot is None else rot
+        rot = head_dim
     else:
         for name, t in (("q_gamma", q_gamma), ("k_gamma", k_gamma)):
             _require_gpu_bf16(name, t)
-        for name, t, dt in (("pos", pos, torch.float32), ("pair_axis", pair_axis, torch.int32),
-                            ("pair_inv", pair_inv, torch.float32)):
-            if t is None or not t.is_cuda or t.dtype != dt or not t.is_contiguous():
-                raise ValueError(f"{name} must be a contiguous {dt} GPU tensor")
-        rot = rot if rot is not None else 2 * pair_axis.numel()
-        if pos.dim() != 2 or pos.shape[0] < S or pos.shape[1] != 3:
-            raise ValueError(f"pos must be [>= {S}, 3]")
-        if pair_axis.numel() < rot // 2 or pair_inv.numel() < rot // 2:
-            raise ValueError(f"pair tables must hold rot/2 = {rot // 2} entries")
+        dt = torch.bfloat16 if rounding == L.ROUND_REFERENCE else torch.float32
+        if (table is None or not table.is_cuda or table.dtype != dt or not table.is_contiguous()
+                or table.dim() != 4 or table.shape[0] < S or table.shape[2:] != (2, 2)):
+            raise ValueError(f"table must be a contiguous {dt} [>= {S}, rot/2, 2, 2] GPU tensor "
+                             "(rope_table() with the same rounding mode)")
+        rot = 2 * table.shape[1]
     shape = (heads, seq_pad, head_dim)
     if out is None:
         q_out, k_out, v_out = (torch.empty(shape, dtype=torch.bfloat16, device=x.device)
@@ -177,9 +200,9 @@ def qkv_proj(x: torch.Tensor, w: torch.Tensor, q_gamma: torch.Tensor | None = No
             if t.shape != shape or not t.is_contiguous() or t.dtype != torch.bfloat16:
                 raise ValueError("outputs must be contiguous bf16 [heads, seq_pad, head_dim]")
     rc = L.lib().h3hip_qkv_proj(_ptr(x), x.stride(0), _ptr(w), w.stride(0), hidden,
-                                _ptr(q_gamma), _ptr(k_gamma), eps, _ptr(pos), _ptr(pair_axis),
-                                _ptr(pair_inv), rot, rounding, S, seq_pad, heads, head_dim,
-                                _ptr(q_out), _ptr(k_out), _ptr(v_out), _stream(x))
+                                _ptr(q_gamma), _ptr(k_gamma), eps, _ptr(table), rot, rounding,
+                                S, seq_pad, heads, head_dim, _ptr(q_out), _ptr(k_out),
+                                _ptr(v_out), _stream(x))
     if L.check(rc, allow_declined=True) == L.DECLINED:
         return None
     return q_out, k_out, v_out

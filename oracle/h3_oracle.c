@@ -440,6 +440,38 @@ void orc_qk_norm_rope(const uint16_t* x, int64_t ld, int32_t S, int32_t S_pad,
   }
 }
 
+/* H3RoPE.rotationTable(angles(pos, inv_freq)) in the compute dtype
+ * (Sources/H3Modules/H3Transformer.swift:62-78, built once per render at
+ * :271-273): per token s and pair p the 2x2 block [[c, -s], [s, c]] stored
+ * row-major as (c, -s, s, c), with angle = fp32(pos[s][axis[p]]) * inv[p] and
+ * c, s its cos/sin evaluated in double and rounded once to fp32 -- the values
+ * orc_qk_norm_rope rotates with. ORC_ROUND_REFERENCE: bf16 entries (uint16
+ * bit patterns, the bf16 table the reference casts to); ORC_ROUND_FP32: fp32
+ * entries. out holds S * half * 4 entries. */
+void orc_rope_table(const float* pos, int32_t S, const int32_t* pair_axis,
+                    const float* pair_inv, int32_t half, int32_t mode, void* out) {
+  for (int64_t s = 0; s < S; s++) {
+    for (int32_t p = 0; p < half; p++) {
+      float ang = pos[s * 3 + pair_axis[p]] * pair_inv[p];
+      float cf = (float)cos((double)ang), sf = (float)sin((double)ang);
+      int64_t e = (s * half + p) * 4;
+      if (mode == ORC_ROUND_REFERENCE) {
+        uint16_t* o = (uint16_t*)out;
+        o[e] = orc_f32_to_bf16(cf);
+        o[e + 1] = orc_f32_to_bf16(-sf);
+        o[e + 2] = orc_f32_to_bf16(sf);
+        o[e + 3] = orc_f32_to_bf16(cf);
+      } else {
+        float* o = (float*)out;
+        o[e] = cf;
+        o[e + 1] = -sf;
+        o[e + 2] = sf;
+        o[e + 3] = cf;
+      }
+    }
+  }
+}
+
 /* ------------------------------------------------- RoPE tables, positions */
 
 /* Three-axis RoPE for the synthetic benchmark shapes: dim_t/dim_h/dim_w

@@ -83,6 +83,10 @@ void orc_qk_norm_rope(const uint16_t* x, int64_t ld, int32_t S, int32_t S_pad,
                       int32_t H, int32_t D, const uint16_t* gamma, float eps,
                       const float* pos, const int32_t* pair_axis, const float* pair_inv,
                       int32_t rot, int32_t mode, int32_t n_threads, uint16_t* out);
+/* H3RoPE.rotationTable in the compute dtype: (c, -s, s, c) per token and pair,
+ * bf16 bit patterns (REFERENCE) or fp32 (FP32), S * half * 4 entries. */
+void orc_rope_table(const float* pos, int32_t S, const int32_t* pair_axis,
+                    const float* pair_inv, int32_t half, int32_t mode, void* out);
 
 /* ---- RoPE tables and positions (H3Transformer.swift, PackedSequence.swift) ---- */
 int orc_rope_pairs_axes(double theta, int32_t dim_t, int32_t dim_h, int32_t dim_w,

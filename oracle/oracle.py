@@ -111,6 +111,8 @@ def lib() -> ctypes.CDLL:
                                        ctypes.c_int32, ctypes.c_int32, _u16p, ctypes.c_float,
                                        _f32p, _i32p, _f32p, ctypes.c_int32, ctypes.c_int32,
                                        ctypes.c_int32, _u16p]
+        L.orc_rope_table.argtypes = [_f32p, ctypes.c_int32, _i32p, _f32p, ctypes.c_int32,
+                                     ctypes.c_int32, ctypes.c_void_p]
         L.orc_rope_pairs_axes.argtypes = [ctypes.c_double, ctypes.c_int32, ctypes.c_int32,
                                           ctypes.c_int32, _i32p, _f32p]
         L.orc_rope_pairs_h3.argtypes = [_f32p, ctypes.c_int32, _i32p, _f32p]
@@ -310,6 +312,22 @@ def qk_norm_rope(x: np.ndarray, ld: int, S: int, S_pad: int, H: int, D: int,
     lib().orc_qk_norm_rope(_p(x, _u16p), ld, S, S_pad, H, D, _p(gamma, _u16p), eps,
                            _p(pos, _f32p), _p(pair_axis, _i32p), _p(pair_inv, _f32p), rot, mode,
                            threads, _p(out, _u16p))
+    return out
+
+
+def rope_table(pos: np.ndarray, pair_axis: np.ndarray, pair_inv: np.ndarray, rot: int,
+               mode: int = ROUND_REFERENCE) -> np.ndarray:
+    """H3RoPE.rotationTable (H3Transformer.swift:62-78): [S, rot/2, 4] entries
+    (c, -s, s, c); uint16 bf16 bit patterns for REFERENCE, float32 for FP32."""
+    pos = np.ascontiguousarray(pos, dtype=np.float32)
+    pair_axis = np.ascontiguousarray(pair_axis, dtype=np.int32)
+    pair_inv = np.ascontiguousarray(pair_inv, dtype=np.float32)
+    S, half = pos.shape[0], rot // 2
+    if pair_axis.size < half or pair_inv.size < half:
+        raise ValueError(f"pair tables must hold rot/2 = {half} entries")
+    out = np.zeros((S, half, 4), dtype=np.uint16 if mode == ROUND_REFERENCE else np.float32)
+    lib().orc_rope_table(_p(pos, _f32p), S, _p(pair_axis, _i32p), _p(pair_inv, _f32p), half,
+                         mode, out.ctypes.data_as(ctypes.c_void_p))
     return out
 
 

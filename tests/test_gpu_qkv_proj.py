@@ -4,12 +4,13 @@ Two checks per case:
 - the plain GEMM (both gammas NULL) against an fp32 product computed on the
   CPU: each bf16 output within half a bf16 ulp of its fp32 value plus a small
   term for fp32 accumulation order (|d| <= 2^-8 |want| + 1e-3 rms);
-- the fused call against h3hip_qk_norm_rope applied to the plain GEMM's
-  output (converted back to the token-major qkv the reference's
-  AttentionLayer.callAsFunction produces, DiTBlock.swift:338-345): Q and K
-  bit-identical, V bit-identical to the plain V. The prologue kernel is itself
-  pinned to the oracle by test_gpu_prologue.py, so this carries the oracle
-  through to the fused kernel.
+- the fused call, rotating with the table h3hip_rope_table builds, against
+  h3hip_qk_norm_rope applied to the plain GEMM's output (converted back to
+  the token-major qkv the reference's AttentionLayer.callAsFunction produces,
+  DiTBlock.swift:338-345): Q and K bit-identical, V bit-identical to the
+  plain V. The prologue kernel is itself pinned to the oracle by
+  test_gpu_prologue.py, so this carries the oracle through to the fused
+  kernel. The table itself is checked against orc_rope_table.
 """
 import numpy as np
 import pytest
@@ -74,9 +75,10 @@ def _run(orc, S, hidden, H, rot, rounding, h3_tables=False, ldx=None, seed=7):
     note(f"qkv_proj plain S={S} hidden={hidden} H={H} ldx={x.stride(0)}")
     plain = ops.qkv_proj(x, w, heads=H)
     torch.cuda.synchronize()
+    note(f"rope_table S={S} rot={rot} rounding={rounding}")
+    table = ops.rope_table(pos, axis, inv, rot=rot, rounding=rounding)
     note(f"qkv_proj fused S={S} hidden={hidden} H={H} rot={rot} rounding={rounding}")
-    fused = ops.qkv_proj(x, w, qg, kg, pos, axis, inv, heads=H, eps=1e-6, rot=rot,
-                         rounding=rounding)
+    fused = ops.qkv_proj(x, w, qg, kg, table, heads=H, eps=1e-6, rounding=rounding)
     torch.cuda.synchronize()
     note(f"prologue over the plain GEMM S={S} H={H}")
     q_tm, k_tm = _token_major(plain[0], S), _token_major(plain[1], S)
@@ -130,7 +132,7 @@ def test_cfg3_full_size(h3, orc):
     rows = np.unique(np.concatenate([np.arange(4), np.arange(S - 4, S), rng.integers(0, S, 60)]))
     _check_plain(*plain, x, w, S, rows=rows)
     note("qkv_proj cfg3 fused")
-    fused = ops.qkv_proj(x, w, qg, kg, pos, axis, inv, heads=H, eps=1e-6)
+    fused = ops.qkv_proj(x, w, qg, kg, ops.rope_table(pos, axis, inv), heads=H, eps=1e-6)
     torch.cuda.synchronize()
     assert np.array_equal(bits(fused[2]), bits(plain[2]))
     q_tm = _token_major(plain[0], S)
@@ -143,6 +145,36 @@ def test_cfg3_full_size(h3, orc):
     assert torch.equal(fused[1].view(torch.int16), want_k.view(torch.int16))
 
 
+@pytest.mark.parametrize("rot,rounding,h3t", [(128, 0, False), (128, 1, False), (96, 0, True),
+                                               (96, 1, True)])
+def test_rope_table_matches_oracle(h3, orc, rot, rounding, h3t):
+    """h3hip_rope_table against orc_rope_table (cos/sin in double, rounded
+    once): bf16 entries identical; fp32 entries within 2 ulp (the device
+    sincosf is not correctly rounded); the [[c, -s], [s, c]] structure exact."""
+    from h3hip import ops
+    S = 300
+    pos, axis, inv = _tables(orc, S, rot, h3t)
+    pos = pos + 0.25 * (torch.arange(S, device="cuda", dtype=torch.float32)[:, None] % 3)
+    note(f"rope_table vs oracle rot={rot} rounding={rounding}")
+    got = ops.rope_table(pos, axis, inv, rot=rot, rounding=rounding)
+    torch.cuda.synchronize()
+    want = orc.rope_table(pos.cpu().numpy(), axis.cpu().numpy(), inv.cpu().numpy(), rot, rounding)
+    assert got.shape == (S, rot // 2, 2, 2)
+    g = got.reshape(S, rot // 2, 4)
+    if rounding == 0:
+        gb = g.view(torch.int16).cpu().numpy().view(np.uint16)
+        same = np.mean(gb == want)
+        print(f"rope table bf16 identical {same:.6f}")
+        assert same >= 0.999
+        assert np.array_equal(gb[..., 0], gb[..., 3]) and np.array_equal(gb[..., 1], gb[..., 2] ^ 0x8000)
+    else:
+        gf = g.cpu().numpy()
+        ulp = np.abs(gf.view(np.int32).astype(np.int64) - want.view(np.int32).astype(np.int64))
+        print(f"rope table fp32 max ulp {ulp.max()}")
+        assert ulp.max() <= 2
+        assert np.array_equal(gf[..., 0], gf[..., 3]) and np.array_equal(gf[..., 1], -gf[..., 2])
+
+
 def test_declines_and_refusals(h3):
     from h3hip import ops
     from h3hip._lib import H3HIPError
@@ -152,9 +184,9 @@ def test_declines_and_refusals(h3):
                                        device="cuda"), heads=3) is None
     assert ops.qkv_proj(x, torch.zeros((3 * 2 * 64, 128), dtype=torch.bfloat16, device="cuda"),
                         heads=2, head_dim=64) is None
-    # hidden not a multiple of 64 declines.
-    x2 = torch.zeros((16, 96), dtype=torch.bfloat16, device="cuda")
-    assert ops.qkv_proj(x2, torch.zeros((768, 96), dtype=torch.bfloat16, device="cuda"),
+    # hidden not a multiple of 32 declines.
+    x2 = torch.zeros((16, 80), dtype=torch.bfloat16, device="cuda")
+    assert ops.qkv_proj(x2, torch.zeros((768, 80), dtype=torch.bfloat16, device="cuda"),
                         heads=2) is None
     # seq_pad not a multiple of 128 is an error.
     with pytest.raises(H3HIPError):

@@ -170,3 +170,55 @@ def test_positions_packed_matches_packed_layout(orc):
     assert np.allclose(video[0, 0, :, 2], w_axis, rtol=0, atol=1e-12)
     # The lattice identity (PackedLayoutTests.swift:62-81): spans cover 124 frames.
     assert sum([1, 4, 4, 4, 4][k % 5] for k in range(37)) == 124
+
+
+@pytest.mark.parametrize("rot,h3", [(128, False), (96, True)])
+def test_rope_table_pins(orc, rot, h3):
+    """orc_rope_table (H3RoPE.rotationTable, H3Transformer.swift:62-78): the
+    [[c, -s], [s, c]] structure, identity at position 0, points on the unit
+    circle, REFERENCE entries = bf16 of the FP32 entries, and -- tying it to
+    the pinned prologue oracle -- rotating the position-0 (unrotated) output
+    of orc_qk_norm_rope with the table's entries in numpy reproduces its
+    rotated output bit for bit. A swapped sign, a c/s swap or a wrong pair ->
+    axis mapping fails the last check."""
+    S, H, D = 37, 3, 128
+    x, gamma, pos = make_inputs(orc, S, H, D, seed=5)
+    pos = pos + np.float32(0.37) * (np.arange(S, dtype=np.float32)[:, None] % 5)  # non-integer too
+    pos[:5] = 0.0
+    if h3:
+        axis, inv = orc.rope_pairs_h3((1.0 / 10000.0 ** (np.arange(16) / 16)).astype(np.float32))
+    else:
+        axis, inv = orc.rope_pairs_axes(10000.0, 32, 48, 48)
+    axis, inv = axis[:rot // 2], inv[:rot // 2]
+    half = rot // 2
+    tr = orc.rope_table(pos, axis, inv, rot, orc.ROUND_REFERENCE)
+    tf = orc.rope_table(pos, axis, inv, rot, orc.ROUND_FP32)
+    assert tr.shape == (S, half, 4) and tr.dtype == np.uint16
+    assert tf.shape == (S, half, 4) and tf.dtype == np.float32
+    # Structure.
+    assert np.array_equal(tr[..., 0], tr[..., 3]) and np.array_equal(tr[..., 1], tr[..., 2] ^ 0x8000)
+    assert np.array_equal(tf[..., 0], tf[..., 3]) and np.array_equal(tf[..., 1], -tf[..., 2])
+    # Position 0 is the identity rotation.
+    assert np.all(tf[:5, :, 0] == 1.0) and np.all(tf[:5, :, 2] == 0.0)
+    # Unit circle (fp32 cos and sin, each rounded once).
+    c, s = tf[..., 0].astype(np.float64), tf[..., 2].astype(np.float64)
+    assert np.max(np.abs(c * c + s * s - 1.0)) < 4e-7
+    # REFERENCE = bf16(FP32).
+    assert np.array_equal(tr, orc.f32_to_bf16(tf))
+    # Tie to orc_qk_norm_rope: rotate its unrotated output with the table.
+    unrot = orc.qk_norm_rope(x, H * D, S, S, H, D, gamma, 1e-6, np.zeros_like(pos), axis, inv,
+                             rot, orc.ROUND_REFERENCE)
+    want = orc.qk_norm_rope(x, H * D, S, S, H, D, gamma, 1e-6, pos, axis, inv, rot,
+                            orc.ROUND_REFERENCE)
+    a = orc.bf16_to_f32(unrot[..., :half])
+    b = orc.bf16_to_f32(unrot[..., half:rot])
+    tc = orc.bf16_to_f32(tr[..., 0])[None]      # [1, S, half]
+    tns = orc.bf16_to_f32(tr[..., 1])[None]
+    ts = orc.bf16_to_f32(tr[..., 2])[None]
+    rb = lambda t: orc.bf16_to_f32(orc.f32_to_bf16(t.astype(np.float32)))
+    got = unrot.copy()
+    got[..., :half] = orc.f32_to_bf16(rb(rb(tc * a) + rb(tns * b)))
+    got[..., half:rot] = orc.f32_to_bf16(rb(rb(ts * a) + rb(tc * b)))
+    assert np.array_equal(got, want)
+    # The rotation is not trivially the identity on these inputs.
+    assert not np.array_equal(unrot, want)
