@@ -256,6 +256,9 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
     }
   }
   __builtin_amdgcn_s_waitcnt(kPWaitVmcnt0);
+  // Every wave is past its last LDS read and its loads have landed: the ring
+  // is free for the output transpose.
+  __syncthreads();
 
   // ---- epilogue: lane (li, hh) holds token m0 + 64mq + 32mb + li, channels
   // 32nb + 8g + 4hh + e of the head in register 4g + e of acc[nb][mb], i.e.
@@ -265,12 +268,22 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   const uint16_t* gamma = part == 0 ? a.q_gamma : a.k_gamma;
   constexpr int hl = kHl;
   constexpr int half = 8 * kHl;            // rot / 2
+  // Output transpose: the wave's 32 x 128 block goes through its own 8 KiB of
+  // LDS, written as 8-byte slots (2c + hh) ^ li of row li (conflict-free), and
+  // read back 16 bytes per lane as whole rows, so each global store writes
+  // 1 KiB contiguous (4 rows of the head-major output) instead of 16-byte
+  // pieces of 32 rows.
+  uint16_t* blk = lds + wave * (32 * kHD);
+  auto put = [&](int c, uint32_t w0, uint32_t w1) __attribute__((always_inline)) {
+    const u32x2 v2 = {w0, w1};
+    *reinterpret_cast<u32x2*>(blk + li * kHD + (((2 * c + hh) ^ li) * 4)) = v2;
+  };
 #pragma unroll
   for (int mb = 0; mb < kMB; mb++) {
-    const int m = m0 + kTokWave * mq + 32 * mb + li;
-    if (m >= a.seq_pad) continue;
+    const int mrow0 = m0 + kTokWave * mq + 32 * mb;   // first row of the block (wave-uniform)
+    if (mrow0 >= a.seq_pad) continue;
+    const int m = mrow0 + li;
     const bool valid = m < a.seq_len;
-    uint16_t* row = out + ((int64_t)head * a.seq_pad + m) * kHD + 4 * hh;
     // bf16 GEMM result of this lane's half-chunks, packed: xb[c][0..1].
     uint32_t xb[16][2];
 #pragma unroll
@@ -280,103 +293,111 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
     }
     if (!norm) {
 #pragma unroll
-      for (int c = 0; c < 16; c++) {
-        const u32x2 v2 = {valid ? xb[c][0] : 0u, valid ? xb[c][1] : 0u};
-        *reinterpret_cast<u32x2*>(row + 8 * c) = v2;
+      for (int c = 0; c < 16; c++) put(c, valid ? xb[c][0] : 0u, valid ? xb[c][1] : 0u);
+    } else {
+      // Mean of squares in the prologue's order: per slot j an fma chain over
+      // chunk a then chunk b, channel order within a chunk, then ((s0+s7)+(s2+s5))
+      // + ((s1+s6)+(s3+s4)). The lower half-wave runs slots 0..3, the upper
+      // slots 4..7: permlane32_swap(x, y) leaves the lower half-wave's word of x
+      // in [0] and the lower half-wave's word of y in [0]'s upper lanes, the
+      // upper half-wave's words in [1], so with x = chunk c of slot j and y =
+      // chunk c' of slot j + 4 every lane gets channels 0..3 of its chunk in
+      // [0] and 4..7 in [1] -- one swap per word for both half-waves.
+      auto pair_sq = [&](int c, int c2, float acc_s) __attribute__((always_inline)) {
+        const auto w0 = __builtin_amdgcn_permlane32_swap(xb[c][0], xb[c2][0], false, false);
+        const auto w1 = __builtin_amdgcn_permlane32_swap(xb[c][1], xb[c2][1], false, false);
+        const uint32_t wd[4] = {w0[0], w1[0], w0[1], w1[1]};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float v0 = bf16_lo(wd[q]), v1 = bf16_hi(wd[q]);
+          acc_s = fmaf(v0, v0, acc_s);
+          acc_s = fmaf(v1, v1, acc_s);
+        }
+        return acc_s;
+      };
+      auto slot_a = [&](int j) { return j < hl ? j : 2 * hl + 2 * (j - hl); };
+      auto slot_b = [&](int j) { return j < hl ? j + hl : 2 * hl + 2 * (j - hl) + 1; };
+      float sj[8];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        // This lane's slot: j (lower half-wave) or j + 4 (upper).
+        const float mine =
+            pair_sq(slot_b(j), slot_b(j + 4), pair_sq(slot_a(j), slot_a(j + 4), 0.f));
+        const auto both = __builtin_amdgcn_permlane32_swap(__float_as_uint(mine),
+                                                           __float_as_uint(mine), false, false);
+        sj[j] = __uint_as_float(both[0]);
+        sj[j + 4] = __uint_as_float(both[1]);
       }
-      continue;
-    }
-    // Mean of squares in the prologue's order: per slot j an fma chain over
-    // chunk a then chunk b, channel order within a chunk, then ((s0+s7)+(s2+s5))
-    // + ((s1+s6)+(s3+s4)). The lower half-wave runs slots 0..3, the upper
-    // slots 4..7: permlane32_swap(x, y) leaves the lower half-wave's word of x
-    // in [0] and the lower half-wave's word of y in [0]'s upper lanes, the
-    // upper half-wave's words in [1], so with x = chunk c of slot j and y =
-    // chunk c' of slot j + 4 every lane gets channels 0..3 of its chunk in
-    // [0] and 4..7 in [1] -- one swap per word for both half-waves.
-    auto pair_sq = [&](int c, int c2, float acc_s) __attribute__((always_inline)) {
-      const auto w0 = __builtin_amdgcn_permlane32_swap(xb[c][0], xb[c2][0], false, false);
-      const auto w1 = __builtin_amdgcn_permlane32_swap(xb[c][1], xb[c2][1], false, false);
-      const uint32_t wd[4] = {w0[0], w1[0], w0[1], w1[1]};
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float v0 = bf16_lo(wd[q]), v1 = bf16_hi(wd[q]);
-        acc_s = fmaf(v0, v0, acc_s);
-        acc_s = fmaf(v1, v1, acc_s);
-      }
-      return acc_s;
-    };
-    auto slot_a = [&](int j) { return j < hl ? j : 2 * hl + 2 * (j - hl); };
-    auto slot_b = [&](int j) { return j < hl ? j + hl : 2 * hl + 2 * (j - hl) + 1; };
-    float sj[8];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      // This lane's slot: j (lower half-wave) or j + 4 (upper).
-      const float mine =
-          pair_sq(slot_b(j), slot_b(j + 4), pair_sq(slot_a(j), slot_a(j + 4), 0.f));
-      const auto both = __builtin_amdgcn_permlane32_swap(__float_as_uint(mine),
-                                                         __float_as_uint(mine), false, false);
-      sj[j] = __uint_as_float(both[0]);
-      sj[j + 4] = __uint_as_float(both[1]);
-    }
-    const float tot = ((sj[0] + sj[7]) + (sj[2] + sj[5])) + ((sj[1] + sj[6]) + (sj[3] + sj[4]));
-    const float r = rsqrt_rounded(tot * (1.0f / kHD) + a.eps);
-    // Normalised values of this lane's half-chunk c: (x r) gamma.
-    auto norm4 = [&](int c, float y[4]) __attribute__((always_inline)) {
-      const u32x2 g2 = *reinterpret_cast<const u32x2*>(gamma + 8 * c + 4 * hh);
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const uint32_t xw = xb[c][e >> 1], gw = g2[e >> 1];
-        const float xv = (e & 1) ? bf16_hi(xw) : bf16_lo(xw);
-        const float gv = (e & 1) ? bf16_hi(gw) : bf16_lo(gw);
-        y[e] = (xv * r) * gv;
-      }
-    };
-    auto store4 = [&](int c, const float o[4]) __attribute__((always_inline)) {
-      const u32x2 v2 = {valid ? cvt_pk(o[0], o[1]) : 0u, valid ? cvt_pk(o[2], o[3]) : 0u};
-      *reinterpret_cast<u32x2*>(row + 8 * c) = v2;
-    };
-    // Table row of this token (row 0 for padding rows, whose output is zero).
-    const int64_t trow = (int64_t)(valid ? m : 0) * half;
-#pragma unroll
-    for (int c = 0; c < hl; c++) {
-      // Pairs p = 8c + 4hh + e rotate channels p (chunk c) and p + rot/2
-      // (chunk c + hl), both in this lane.
-      RopeEntry te[4];
-      if (kMode == H3HIP_ROUND_REFERENCE) {
-        const u32x4* tp = reinterpret_cast<const u32x4*>(
-            static_cast<const uint16_t*>(a.table) + (trow + 8 * c + 4 * hh) * 4);
-        const u32x4 t01 = tp[0], t23 = tp[1];   // (c, -s, s, c) bf16 of pairs e
+      const float tot = ((sj[0] + sj[7]) + (sj[2] + sj[5])) + ((sj[1] + sj[6]) + (sj[3] + sj[4]));
+      const float r = rsqrt_rounded(tot * (1.0f / kHD) + a.eps);
+      // Normalised values of this lane's half-chunk c: (x r) gamma.
+      auto norm4 = [&](int c, float y[4]) __attribute__((always_inline)) {
+        const u32x2 g2 = *reinterpret_cast<const u32x2*>(gamma + 8 * c + 4 * hh);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const u32x4& tv = e < 2 ? t01 : t23;
-          const int o = 2 * (e & 1);
-          te[e] = RopeEntry{bf16_lo(tv[o]), bf16_lo(tv[o + 1])};
+          const uint32_t xw = xb[c][e >> 1], gw = g2[e >> 1];
+          const float xv = (e & 1) ? bf16_hi(xw) : bf16_lo(xw);
+          const float gv = (e & 1) ? bf16_hi(gw) : bf16_lo(gw);
+          y[e] = (xv * r) * gv;
         }
-      } else {
-        const f32x4* tp = reinterpret_cast<const f32x4*>(a.table) + trow + 8 * c + 4 * hh;
+      };
+      auto store4 = [&](int c, const float o[4]) __attribute__((always_inline)) {
+        put(c, valid ? cvt_pk(o[0], o[1]) : 0u, valid ? cvt_pk(o[2], o[3]) : 0u);
+      };
+      // Table row of this token (row 0 for padding rows, whose output is zero).
+      const int64_t trow = (int64_t)(valid ? m : 0) * half;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const f32x4 tv = tp[e];
-          te[e] = RopeEntry{tv[0], tv[2]};
+      for (int c = 0; c < hl; c++) {
+        // Pairs p = 8c + 4hh + e rotate channels p (chunk c) and p + rot/2
+        // (chunk c + hl), both in this lane.
+        RopeEntry te[4];
+        if (kMode == H3HIP_ROUND_REFERENCE) {
+          const u32x4* tp = reinterpret_cast<const u32x4*>(
+              static_cast<const uint16_t*>(a.table) + (trow + 8 * c + 4 * hh) * 4);
+          const u32x4 t01 = tp[0], t23 = tp[1];   // (c, -s, s, c) bf16 of pairs e
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const u32x4& tv = e < 2 ? t01 : t23;
+            const int o = 2 * (e & 1);
+            te[e] = RopeEntry{bf16_lo(tv[o]), bf16_lo(tv[o + 1])};
+          }
+        } else {
+          const f32x4* tp = reinterpret_cast<const f32x4*>(a.table) + trow + 8 * c + 4 * hh;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const f32x4 tv = tp[e];
+            te[e] = RopeEntry{tv[0], tv[2]};
+          }
         }
+        float ya[4], yb[4], oa[4], ob[4];
+        norm4(c, ya);
+        norm4(c + hl, yb);
+#pragma unroll
+        for (int e = 0; e < 4; e++) rope_pair<kMode>(ya[e], yb[e], te[e], true, oa[e], ob[e]);
+        store4(c, oa);
+        store4(c + hl, ob);
       }
-      float ya[4], yb[4], oa[4], ob[4];
-      norm4(c, ya);
-      norm4(c + hl, yb);
+      // Channels >= rot pass through (bf16-rounded as in the prologue).
 #pragma unroll
-      for (int e = 0; e < 4; e++) rope_pair<kMode>(ya[e], yb[e], te[e], true, oa[e], ob[e]);
-      store4(c, oa);
-      store4(c + hl, ob);
+      for (int c = 2 * hl; c < 16; c++) {
+        float y[4], o[4];
+        norm4(c, y);
+        rope_pair<kMode>(y[0], y[1], RopeEntry{1.f, 0.f}, false, o[0], o[1]);
+        rope_pair<kMode>(y[2], y[3], RopeEntry{1.f, 0.f}, false, o[2], o[3]);
+        store4(c, o);
+      }
     }
-    // Channels >= rot pass through (bf16-rounded as in the prologue).
+    // Row r = 4i + lane / 16, chunk k = lane % 16: slots 2k, 2k + 1 sit at
+    // (2k ^ r) and (2k + 1) ^ r, i.e. the 16-byte word at 2k ^ (r & 30) with
+    // its halves swapped when r is odd.
+    uint16_t* dst = out + ((int64_t)head * a.seq_pad + mrow0) * kHD;
+    const int k = lane & 15;
 #pragma unroll
-    for (int c = 2 * hl; c < 16; c++) {
-      float y[4], o[4];
-      norm4(c, y);
-      rope_pair<kMode>(y[0], y[1], RopeEntry{1.f, 0.f}, false, o[0], o[1]);
-      rope_pair<kMode>(y[2], y[3], RopeEntry{1.f, 0.f}, false, o[2], o[3]);
-      store4(c, o);
+    for (int i = 0; i < 8; i++) {
+      const int r = 4 * i + (lane >> 4);
+      u32x4 v = *reinterpret_cast<const u32x4*>(blk + r * kHD + ((2 * k) ^ (r & 30)) * 4);
+      if (r & 1) v = u32x4{v[2], v[3], v[0], v[1]};
+      if (mrow0 + r < a.seq_pad) *reinterpret_cast<u32x4*>(dst + r * kHD + 8 * k) = v;
     }
   }
 }
