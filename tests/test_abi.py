@@ -89,3 +89,37 @@ def test_prologue_declines_unsupported_geometry(h3):
     rc = lib.h3hip_qk_norm_rope(None, None, 768, None, None, None, 1e-5, None, None, None, 100,
                                 0, 4, 4, 2, 128, None, None, None, None)
     assert rc == _lib.DECLINED
+
+
+def test_projection_and_rope_table_refusals(h3):
+    """h3hip_qkv_proj declines geometry it does not handle (the caller then runs
+    its own GEMM + prologue) and refuses bad arguments by name; h3hip_rope_table
+    refuses NULL and odd rot -- all before any device call."""
+    from h3hip import _lib
+    lib = h3.lib()
+    D = _lib.DECLINED
+    # head_dim 64, rot 80, odd heads, hidden % 64: declined.
+    for head_dim, rot, heads, hidden in ((64, 64, 2, 128), (128, 80, 2, 128), (128, 128, 3, 128),
+                                         (128, 128, 2, 96)):
+        rc = lib.h3hip_qkv_proj(None, hidden, None, hidden, hidden, None, None, 1e-6, None, rot,
+                                0, 4, 128, heads, head_dim, None, None, None, None)
+        assert rc == D, (head_dim, rot, heads, hidden)
+        assert "declined" in h3.last_error()
+    # Supported geometry, NULL tensors: refused.
+    rc = lib.h3hip_qkv_proj(None, 128, None, 128, 128, None, None, 1e-6, None, 128, 0, 4, 128, 2,
+                            128, None, None, None, None)
+    assert rc == _lib.EINVAL and "NULL" in h3.last_error()
+    # Gammas given without a rotation table: refused.
+    buf = ctypes.c_void_p(16)
+    rc = lib.h3hip_qkv_proj(buf, 128, buf, 128, 128, buf, buf, 1e-6, None, 128, 0, 4, 128, 2,
+                            128, buf, buf, buf, None)
+    assert rc == _lib.EINVAL and "rotation table" in h3.last_error()
+    # seq_pad not a multiple of 128: refused.
+    rc = lib.h3hip_qkv_proj(buf, 128, buf, 128, 128, None, None, 1e-6, None, 128, 0, 4, 144, 2,
+                            128, buf, buf, buf, None)
+    assert rc == _lib.EINVAL and "seq_pad" in h3.last_error()
+    assert lib.h3hip_rope_table(None, None, None, 128, 0, 4, None, None) == _lib.EINVAL
+    rc = lib.h3hip_rope_table(buf, buf, buf, 127, 0, 4, buf, None)
+    assert rc == _lib.EINVAL and "rot" in h3.last_error()
+    rc = lib.h3hip_rope_table(buf, buf, buf, 128, 7, 4, buf, None)
+    assert rc == _lib.EINVAL and "rounding" in h3.last_error()
