@@ -34,13 +34,13 @@ def _tables(orc, S, rot, h3_tables):
             torch.from_numpy(inv).cuda())
 
 
-def _inputs(S, hidden, H, seed, ldx=None):
+def _inputs(S, hidden, H, seed, ldx=None, ldw=None):
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
-    ldx = ldx or hidden
+    ldx, ldw = ldx or hidden, ldw or hidden
     xb = torch.randn((S, ldx), generator=g, device="cuda").to(torch.bfloat16)
-    w = (torch.randn((3 * H * 128, hidden), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
-    return xb[:, :hidden], w
+    w = (torch.randn((3 * H * 128, ldw), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    return xb[:, :hidden], w[:, :hidden]
 
 
 def _token_major(t, S):
@@ -66,9 +66,9 @@ def _check_plain(q, k, v, x, w, S, rows=None):
         assert torch.all(t[:, S:] == 0)
 
 
-def _run(orc, S, hidden, H, rot, rounding, h3_tables=False, ldx=None, seed=7):
+def _run(orc, S, hidden, H, rot, rounding, h3_tables=False, ldx=None, seed=7, ldw=None):
     from h3hip import ops
-    x, w = _inputs(S, hidden, H, seed, ldx)
+    x, w = _inputs(S, hidden, H, seed, ldx, ldw)
     qg = to_gpu_bf16(orc.uniform_bf16((128,), seed + 1, 0.9, 1.1))
     kg = to_gpu_bf16(orc.uniform_bf16((128,), seed + 2, 0.9, 1.1))
     pos, axis, inv = _tables(orc, S, rot, h3_tables)
@@ -93,7 +93,8 @@ def _run(orc, S, hidden, H, rot, rounding, h3_tables=False, ldx=None, seed=7):
     (300, 256, 2, 128, 1, False),     # fp32 rounding
     (256, 512, 4, 96, 0, True),       # the H3 table: rot 96, channels 96..127 pass through
     (130, 128, 6, 96, 1, True),       # S just past one 128-row tile, rot 96 fp32 rounding
-    (1000, 5120, 4, 128, 0, False),   # the model's hidden width
+    (1000, 5120, 4, 128, 0, False),   # the benchmark configs' hidden width
+    (700, 5376, 56, 96, 0, True),     # the H3 model: hidden 5,376, 56 heads, rot 96
 ])
 def test_fused_equals_prologue_of_plain(h3, orc, S, hidden, H, rot, rounding, h3t):
     x, w, plain, fused, (want_q, want_k) = _run(orc, S, hidden, H, rot, rounding, h3t)
@@ -104,10 +105,10 @@ def test_fused_equals_prologue_of_plain(h3, orc, S, hidden, H, rot, rounding, h3
     assert np.array_equal(bits(v), bits(plain[2]))
 
 
-def test_strided_x_rows(h3, orc):
-    """x as a view with row stride > hidden (e.g. a slice of a wider buffer)."""
-    x, w, plain, fused, (want_q, want_k) = _run(orc, 200, 384, 2, 128, 0, ldx=1024)
-    assert x.stride(0) == 1024
+def test_strided_x_and_w_rows(h3, orc):
+    """x and W as views with row stride > hidden (slices of wider buffers)."""
+    x, w, plain, fused, (want_q, want_k) = _run(orc, 200, 384, 2, 128, 0, ldx=1024, ldw=448)
+    assert x.stride(0) == 1024 and w.stride(0) == 448
     _check_plain(*plain, x, w, 200)
     assert np.array_equal(bits(fused[0]), bits(want_q))
     assert np.array_equal(bits(fused[1]), bits(want_k))
@@ -143,6 +144,27 @@ def test_cfg3_full_size(h3, orc):
     torch.cuda.synchronize()
     assert torch.equal(fused[0].view(torch.int16), want_q.view(torch.int16))
     assert torch.equal(fused[1].view(torch.int16), want_k.view(torch.int16))
+
+
+def test_larger_seq_pad_is_zero_filled(h3, orc):
+    """A caller's seq_pad beyond the 128-row round-up: rows seq_len .. seq_pad
+    of Q, K and V come out zero, rows below are the same as with the minimal
+    seq_pad."""
+    from h3hip import ops
+    S, H = 150, 2
+    x, w = _inputs(S, 256, H, 9)
+    qg = to_gpu_bf16(orc.uniform_bf16((128,), 10, 0.9, 1.1))
+    kg = to_gpu_bf16(orc.uniform_bf16((128,), 11, 0.9, 1.1))
+    pos, axis, inv = _tables(orc, S, 128, False)
+    table = ops.rope_table(pos, axis, inv)
+    note("qkv_proj seq_pad 512 vs 256")
+    big = [torch.full((H, 512, 128), 7.0, dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+    ops.qkv_proj(x, w, qg, kg, table, heads=H, seq_pad=512, out=tuple(big))
+    small = ops.qkv_proj(x, w, qg, kg, table, heads=H, seq_pad=256)
+    torch.cuda.synchronize()
+    for b, sm in zip(big, small):
+        assert torch.all(b[:, S:] == 0)
+        assert torch.equal(b[:, :S].view(torch.int16), sm[:, :S].view(torch.int16))
 
 
 @pytest.mark.parametrize("rot,rounding,h3t", [(128, 0, False), (128, 1, False), (96, 0, True),
