@@ -192,6 +192,64 @@ def qkv_projection_extra(args, env):
             "gemm_tflop": round(flops / 1e12, 4)}
 
 
+def attention_layer_extra(args, env):
+    """AttentionLayer.callAsFunction (DiTBlock.swift:336-359) at config 3, end to
+    end: QKV projection + Q/K norm/RoPE, block-sparse attention, out-projection
+    (a plain GEMM, hipBLASLt via torch.mm in both paths). Two paths for the
+    first part: the fused projection kernel, or hipBLASLt's GEMM followed by
+    the prologue kernel (V then read in place from the token-major qkv)."""
+    import numpy as np
+    import torch
+    from h3hip import ops
+    H, D, S, S_pad = env["H"], env["D"], env["S"], env["S_pad"]
+    inner = H * D
+    x, w = qkv_inputs(env)
+    g, dev = env["g"], env["dev"]
+    w_out = (torch.randn((C_HIDDEN, inner), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    plan, scale = env["plan"], env["scale"]
+    qh, kh = env["qh"], env["kh"]
+    vh = torch.empty_like(qh)
+    qkv = torch.empty((S, 3 * inner), dtype=torch.bfloat16, device=dev)
+    att = torch.empty((S, inner), dtype=torch.bfloat16, device=dev)
+    att_view = att.view(S, H, D).transpose(0, 1)
+    v_view = qkv[:, 2 * inner:].view(S, H, D).transpose(0, 1)
+    y = torch.empty((S, C_HIDDEN), dtype=torch.bfloat16, device=dev)
+    table = ops.rope_table(env["pos"], env["ax"], env["inv"])
+    eps = env["C"].QK_EPS
+
+    def fused_path():
+        ops.qkv_proj(x, w, env["gq"], env["gk"], table, heads=H, eps=eps, seq_pad=S_pad,
+                     out=(qh, kh, vh))
+        ops.bsattn_fwd_strided(plan, qh, kh, vh, scale, out=att_view)
+        torch.mm(att, w_out.t(), out=y)
+
+    def unfused_path():
+        torch.mm(x, w.t(), out=qkv)
+        ops.qk_norm_rope(qkv[:, :inner], qkv[:, inner:2 * inner], env["gq"], env["gk"],
+                         env["pos"], env["ax"], env["inv"], heads=H, eps=eps, seq_pad=S_pad,
+                         out=(qh, kh, None))
+        ops.bsattn_fwd_strided(plan, qh, kh, v_view, scale, out=att_view)
+        torch.mm(att, w_out.t(), out=y)
+
+    res = {}
+    for name, f in (("fused_qkv", fused_path), ("hipblaslt_qkv", unfused_path)):
+        reps = max(10, args.steps)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps + 2)]
+        for a, b in ev:
+            a.record()
+            f()
+            b.record()
+        torch.cuda.synchronize()
+        res[name + "_ms"] = round(float(np.mean([a.elapsed_time(b) for a, b in ev[2:]])), 4)
+    flops = (2.0 * S * C_HIDDEN * 3 * inner + plan.nnz * H * FLOP_PER_TILE_HEAD
+             + 2.0 * S * inner * C_HIDDEN)
+    res["layer_tflop"] = round(flops / 1e12, 4)
+    best = min(res["fused_qkv_ms"], res["hipblaslt_qkv_ms"])
+    res["best_tflops"] = round(flops / (best * 1e-3) / 1e12, 1)
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -359,6 +417,7 @@ def main() -> int:
         }
         del q_in, k_in
         extras["cfg3_qkv_proj"] = qkv_projection_extra(args, env=locals())
+        extras["cfg3_attention_layer"] = attention_layer_extra(args, env=locals())
         for name in ("cfg3_1344x768x5s_frame0", "cfg2_864x480x7s", "cfg4_dense_864x480x7s",
                      "axial_h3_864x480x124"):
             sh = C.ALL[name]
