@@ -1,7 +1,9 @@
 // Block-sparse flash attention over 128x128 tiles, bf16 MFMA on gfx950.
 //
-// One workgroup of 8 waves per (head, 128-query tile) work unit, one
-// workgroup per CU, launched in the plan's XCD-aware order. Waves w and w+4
+// Persistent workgroups of 8 waves, one per CU, each running the (head,
+// 128-query tile) work units that the plan's XCD-aware schedule gives it, one
+// after another; the next unit's first K tile and its Q tile load while the
+// current one merges and stores its output. Waves w and w+4
 // own the same 32 queries (the B operand of v_mfma_f32_32x32x16_bf16, kept in
 // registers) and split every key tile in two 64-key halves, each keeping its
 // own online-softmax state; the halves are merged exactly at the end. The two
@@ -56,6 +58,7 @@ struct AttnArgs {
   uint16_t* __restrict__ out;
   const int32_t* __restrict__ row_ptr;
   const int32_t* __restrict__ col_idx;
+  const int32_t* __restrict__ work_ptr;  // [groups + 1]
   const int32_t* __restrict__ work;
   int64_t q_hs, k_hs, v_hs, o_hs;  // head strides (elements)
   int32_t q_rs, k_rs, v_rs, o_rs;  // row strides (elements)
@@ -101,8 +104,39 @@ __device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& s, int base) {
   return __builtin_convertvector(v, bf16x8);
 }
 
-// Workgroup: 8 waves, one (head, 128-query tile) unit. Wave w owns queries
-// 32*(w&3) .. +31 and key half (w>>2) (keys 64*(w>>2) .. +63) of every tile.
+// A unit's first K tile and its Q tile, HBM -> LDS, issued by one half of the
+// workgroup (wave w moves rows 32(w&3) .. +31 of each, 4 rows per instruction,
+// chunks K-swizzled) into K slot 0 and the Q slot. Buffer resources bound the
+// rows at seq_len, so no row past it is fetched; Q rows past seq_len are
+// replaced by zeros when they are read.
+__device__ __forceinline__ void load_unit_start(const AttnArgs& a, uint16_t* lds, int32_t unit,
+                                                int qg, int lane) {
+  const int head = unit >> 16, qt = unit & 0xffff;
+  const int dma_row = 32 * qg + (lane >> 4);
+  auto tile = [&](const uint16_t* base, int rs2, int row0, uint16_t* slot)
+      __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)base, 0, (a.seq_len - 1) * rs2 + kD * 2, kBufferWord3);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int row = dma_row + 4 * i;
+      const int voff = (row0 + row) * rs2 + (((lane & 15) ^ k_swz(row)) * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc, (lds_void*)(slot + (32 * qg + 4 * i) * kD), 16, voff, 0, 0, 0);
+    }
+  };
+  tile(a.q + head * a.q_hs, a.q_rs * 2, qt * kTile, lds + 4 * kSlot);
+  const int beg = a.row_ptr[qt];
+  if (a.row_ptr[qt + 1] > beg) {
+    const int32_t first_col =
+        *((const __attribute__((address_space(4))) int32_t*)(a.col_idx) + beg);
+    tile(a.k + head * a.k_hs, a.k_rs * 2, first_col * kTile, lds);
+  }
+}
+
+// Workgroup: 8 waves, one (head, 128-query tile) unit at a time. Wave w owns
+// queries 32*(w&3) .. +31 and key half (w>>2) (keys 64*(w>>2) .. +63) of
+// every tile.
 //
 // Ping-pong schedule. Each wave alternates an MFMA phase M_j -- the scores
 // S(j) = K(j) Q^T of tile j and the product O += V(j-1)^T P(j-1) of the
@@ -118,33 +152,28 @@ __device__ __forceinline__ bf16x8 to_bf16x8(const f32x16& s, int base) {
 // V(j) replaces V(j-2), both last read before phase 2j. The MFMA waves thus
 // never have a load in flight, and their LDS operand reads wait for nothing.
 __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
-  // Slots: K(j) at (j & 1) * kSlot, V(j) at (2 + (j & 1)) * kSlot; 128 KiB.
-  __shared__ __attribute__((aligned(16))) uint16_t lds[4 * kSlot];
+  // Slots: K(j) at (j & 1) * kSlot, V(j) at (2 + (j & 1)) * kSlot, the unit's
+  // Q tile at 4 * kSlot; 160 KiB.
+  __shared__ __attribute__((aligned(16))) uint16_t lds[5 * kSlot];
 
-  const int32_t unit = a.work[blockIdx.x];
-  if (unit < 0) return;
-  const int head = unit >> 16, qt = unit & 0xffff;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, in an SGPR
   const int qg = wave & 3, half = wave >> 2;
-  const int li = lane & 31, hh = lane >> 5;
-  const int q0 = qt * kTile + qg * 32;
   const float c = a.scale_log2;
+  const int k_rs2 = a.k_rs * 2, v_rs2 = a.v_rs * 2;
 
-  // Q^T as the B operand: lane (li, hh) holds Q[q0 + li][16s + 8hh .. +7];
-  // query rows past seq_len are not read (zero).
-  bf16x8 qreg[8];
-  {
-    const bool q_valid = q0 + li < a.seq_len;
-    const uint16_t* qrow =
-        a.q + head * a.q_hs + (int64_t)(q_valid ? q0 + li : 0) * a.q_rs + 8 * hh;
-#pragma unroll
-    for (int s = 0; s < 8; s++) {
-      const bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
-      qreg[s] = q_valid ? x : bf16x8{};
-    }
-  }
-
+  // The workgroup's units, one after another (the plan's static schedule).
+  // Waves 4-7 load each unit's K(0) and Q while the previous unit merges and
+  // stores its output; the first unit's here.
+  const int u_beg = a.work_ptr[blockIdx.x], u_end = a.work_ptr[blockIdx.x + 1];
+  if (half == 1 && u_beg < u_end) load_unit_start(a, lds, a.work[u_beg], qg, threadIdx.x & 63);
+  for (int iu = u_beg; iu < u_end; iu++) {
+  // Lane-derived offsets are rebuilt for each unit from an opaque copy of the
+  // thread index: hoisted out of the unit loop they would hold registers that
+  // the operand pipelines of the inner loops need.
+  int tid;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(threadIdx.x));
+  const int lane = tid & 63;
+  const int li = lane & 31, hh = lane >> 5;
   // K operand offsets: block b row half*64 + 32b + li, chunk 2s + hh.
   int k_off[8];
 #pragma unroll
@@ -161,6 +190,29 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
       const int chunk = 4 * db + 2 * (g & 1) + ((mm & 3) >> 1);
       v_off[p][db] = row * kD + ((chunk ^ v_swz(row)) * 8) + 4 * (mm & 1);
     }
+  const int dma_row = 32 * qg + (lane >> 4);
+
+  const int32_t unit = a.work[iu];
+  const int head = unit >> 16, qt = unit & 0xffff;
+  const int q0 = qt * kTile + qg * 32;
+
+  // The unit's K(0) and Q have landed (the loading waves wait for their own
+  // loads), and the previous unit's merge buffers have been read.
+  if (half == 1) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+
+  // Q^T as the B operand, from the Q slot: lane (li, hh) holds
+  // Q[q0 + li][16s + 8hh .. +7]; query rows past seq_len are zero.
+  bf16x8 qreg[8];
+  {
+    const bool q_valid = q0 + li < a.seq_len;
+    const uint16_t* qrow = lds + 4 * kSlot + (qg * 32 + li) * kD;
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + (((2 * s + hh) ^ k_swz(li)) * 8));
+      qreg[s] = q_valid ? x : bf16x8{};
+    }
+  }
 
   // HBM -> LDS by one half of the workgroup, as buffer loads (a per-head
   // resource bounded at row seq_len, 32-bit lane offsets): wave w moves rows
@@ -168,12 +220,10 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
   // position l%16 of row 32(w&3) + 4i + l/16 from the global chunk that the
   // swizzle places there. The whole offset is in the lane offset, which the
   // hardware range-checks, so rows at or past seq_len are never fetched.
-  const int k_rs2 = a.k_rs * 2, v_rs2 = a.v_rs * 2;
   const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.k + head * a.k_hs), 0, (a.seq_len - 1) * k_rs2 + kD * 2, kBufferWord3);
   const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.v + head * a.v_hs), 0, (a.seq_len - 1) * v_rs2 + kD * 2, kBufferWord3);
-  const int dma_row = 32 * qg + (lane >> 4);
   auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int key0, uint16_t* slot,
                  bool v_layout) __attribute__((always_inline)) {
     const int rs2 = v_layout ? v_rs2 : k_rs2;
@@ -295,10 +345,6 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
   };
 
   if (n > 0) {
-    // K(0) by waves 0-3; the Q loads drain with it.
-    if (half == 0) dma(k_rsrc, cols[0] * kTile, lds, false);
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __syncthreads();
     // Each half runs its own loop of two phases per tile (2n + 2 phases and
     // barriers in all), so neither loop merges the other role's state.
     if (half == 0) {
@@ -337,11 +383,13 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
   }
 
   // Merge the two key halves of each query (exact: rescale both to the larger
-  // m). Waves 4-7 leave (O, m, l) in LDS: O in the two K slots, m and l in
-  // the first V slot.
+  // m). Waves 4-7 leave (O, m, l) in LDS -- O in the two V slots, m and l in
+  // K slot 1 -- then, while waves 0-3 merge and store, start the next unit's
+  // K(0) and Q loads into K slot 0 and the Q slot, which no wave reads any
+  // more in this unit.
   const float lt = l + __shfl_xor(l, 32);
-  float* xo = reinterpret_cast<float*>(lds) + qg * 64 * 64;
-  float* xm = reinterpret_cast<float*>(lds + 2 * kSlot);
+  float* xo = reinterpret_cast<float*>(lds + 2 * kSlot) + qg * 64 * 64;
+  float* xm = reinterpret_cast<float*>(lds + kSlot);
   float* xl = xm + 4 * 64;
   if (half == 1) {
 #pragma unroll
@@ -352,7 +400,8 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
     xl[qg * 64 + lane] = lt;
   }
   __syncthreads();
-  if (half == 1) return;
+  if (half == 1 && iu + 1 < u_end) load_unit_start(a, lds, a.work[iu + 1], qg, lane);
+  if (half == 0) {
   const float m1 = xm[qg * 64 + lane], l1 = xl[qg * 64 + lane];
   const float mmax = fmaxf(m, m1);
   const float f0 = __builtin_amdgcn_exp2f(m - mmax), f1 = __builtin_amdgcn_exp2f(m1 - mmax);
@@ -363,25 +412,28 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
   // 32db + 8g + 4hh + [0, 4) in registers 4g .. 4g + 3.
   const int qi = q0 + li;
   const bool valid = qi < a.seq_len;
-  if (qi >= a.out_rows) return;
-  uint16_t* orow = a.out + head * a.o_hs + (int64_t)qi * a.o_rs;
+  if (qi < a.out_rows) {
+    uint16_t* orow = a.out + head * a.o_hs + (int64_t)qi * a.o_rs;
 #pragma unroll
-  for (int db = 0; db < 4; db++)
+    for (int db = 0; db < 4; db++)
 #pragma unroll
-    for (int gg = 0; gg < 4; gg++) {
-      float o[4];
+      for (int gg = 0; gg < 4; gg++) {
+        float o[4];
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int r = 4 * gg + e;
-        o[e] = oacc[db][r] * s0 + xo[(db * 16 + r) * 64 + lane] * s1;
+        for (int e = 0; e < 4; e++) {
+          const int r = 4 * gg + e;
+          o[e] = oacc[db][r] * s0 + xo[(db * 16 + r) * 64 + lane] * s1;
+        }
+        u32x2 w = {0u, 0u};
+        if (valid) {
+          w[0] = pack_bf16x2(o[0], o[1]);
+          w[1] = pack_bf16x2(o[2], o[3]);
+        }
+        *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * gg + 4 * hh) = w;
       }
-      u32x2 w = {0u, 0u};
-      if (valid) {
-        w[0] = pack_bf16x2(o[0], o[1]);
-        w[1] = pack_bf16x2(o[2], o[3]);
-      }
-      *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * gg + 4 * hh) = w;
-    }
+  }
+  }
+  }
 }
 
 // One [heads, rows, 128] view of a caller tensor (strides in elements).
@@ -398,6 +450,7 @@ static int launch_bsattn(h3hip_plan p, const View& q, const View& k, const View&
                 static_cast<uint16_t*>(const_cast<void*>(o.ptr)),
                 p->d_row_ptr,
                 p->d_col_idx,
+                p->d_work_ptr,
                 p->d_work,
                 q.head_stride,
                 k.head_stride,
@@ -410,8 +463,8 @@ static int launch_bsattn(h3hip_plan p, const View& q, const View& k, const View&
                 p->seq_len,
                 out_rows,
                 scale * 1.4426950408889634f};
-  const unsigned grid = (unsigned)p->work.size();
-  if (grid == 0) return H3HIP_OK;
+  const unsigned grid = (unsigned)p->groups;
+  if (p->work.empty()) return H3HIP_OK;
   bsattn_fwd_kernel<<<grid, kThreads, 0, stream>>>(args);
   return check_launch("bsattn_fwd_kernel");
 }
@@ -472,8 +525,8 @@ extern "C" int h3hip_bsattn_fwd_strided(h3hip_plan plan, const h3hip_view* q,
                H3HIP_EINVAL, "%s: row_stride %lld must be a multiple of 8 and >= %d", names[i],
                (long long)t.row_stride, kD);
   }
-  // K and V are fetched with 32-bit offsets from each head's base.
-  for (int i = 1; i < 3; i++)
+  // Q, K and V are fetched with 32-bit offsets from each head's base.
+  for (int i = 0; i < 3; i++)
     H3_REQUIRE((int64_t)plan->seq_pad * views[i]->row_stride * 2 < ((int64_t)1 << 31),
                H3HIP_EINVAL, "%s: seq_pad x row_stride exceeds 32-bit offsets", names[i]);
   auto as_view = [](const h3hip_view* t) { return View{t->data, t->head_stride, t->row_stride}; };

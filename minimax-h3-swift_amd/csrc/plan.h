@@ -18,8 +18,14 @@ struct h3hip_plan_s {
   h3hip_policy policy{};
   std::vector<int32_t> row_ptr;  // host copy [n_tiles + 1]
   std::vector<int32_t> col_idx;  // host copy [nnz]
-  std::vector<int32_t> work;     // launch order: (head << 16 | q_tile) or -1
+  // Attention schedule: one persistent workgroup per CU; workgroup b (on XCD
+  // b % 8) runs the units work[work_ptr[b] .. work_ptr[b + 1]), each
+  // (head << 16 | q_tile), in order.
+  int32_t groups = 0;
+  std::vector<int32_t> work_ptr;  // [groups + 1]
+  std::vector<int32_t> work;
   int32_t* d_row_ptr = nullptr;
   int32_t* d_col_idx = nullptr;
+  int32_t* d_work_ptr = nullptr;
   int32_t* d_work = nullptr;
 };

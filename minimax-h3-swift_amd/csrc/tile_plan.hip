@@ -3,7 +3,8 @@
 // The mask rule is evaluated on the GPU at token level and OR-reduced onto the
 // 128x128 tile grid (one workgroup per tile pair), the bitmap is compacted to
 // CSR by three small kernels (row popcount, single-workgroup scan, ordered
-// fill), and the host derives an XCD-aware launch order from the row lengths.
+// fill), and the host derives the attention kernel's XCD-aware schedule (the
+// units of each persistent workgroup) from the row lengths.
 // Everything here runs once per shape; none of it is on the per-layer path.
 #include <algorithm>
 #include <cstdarg>
@@ -11,6 +12,8 @@
 #include <mutex>
 #include <numeric>
 #include <vector>
+
+#include <queue>
 
 #include "common.h"
 #include "plan.h"
@@ -246,22 +249,28 @@ static int launch_mask(const h3hip_mask_rule* r, uint8_t* d_bitmap, hipStream_t 
   return check_launch("mask_rule_kernel");
 }
 
-// The launch order of (head, q-tile) work units for the attention kernel.
+// The attention kernel's schedule: which (head, q-tile) work units each of
+// its persistent workgroups runs, and in what order.
 //
 // Workgroups are handed to the 8 XCDs round-robin (workgroup b runs on XCD
-// b % 8), and each XCD has its own L2. So each XCD gets its own list, the
-// launch slot s of XCD x is workgroup s*8 + x, and a list is laid out for L2
-// reuse: long rows (the dense prefix rows, ~8x the median) first, grouped by
-// head so that units streaming the same head's K/V run side by side, then a
-// contiguous (head, q-tile) range so neighbouring q-tiles of one head, which
-// share most of their key tiles under local masks, are resident together.
-// Lists are balanced by cost (tiles + a fixed per-unit overhead) and padded
-// with -1 (no-op) to equal length.
-static void build_schedule(const std::vector<int32_t>& row_ptr, int32_t heads,
-                           std::vector<int32_t>& work) {
+// b % 8), and each XCD has its own L2. So each XCD gets its own list, laid
+// out for L2 reuse: long rows (the dense prefix rows, ~8x the median) first,
+// grouped by head so that units streaming the same head's K/V run side by
+// side, then a contiguous (head, q-tile) range so neighbouring q-tiles of one
+// head, which share most of their key tiles under local masks, are resident
+// together. The XCD lists are balanced by cost (tiles + a fixed per-unit
+// overhead). Each list is then dealt to the XCD's workgroups in list order,
+// every unit to the workgroup that the cost model frees first -- the order in
+// which the hardware's own dispatch would hand them out -- so the units an
+// XCD runs at one time stay neighbours in its list.
+// Cost of a unit in tile times beyond its tiles (merge, store, first loads),
+// measured on MI355X (band rules: 1.8 us per tile, the rest per unit).
+constexpr double kUnitOverhead = 2.0;
+
+static void build_schedule(const std::vector<int32_t>& row_ptr, int32_t heads, int32_t groups,
+                           std::vector<int32_t>& work_ptr, std::vector<int32_t>& work) {
   const int32_t nq = (int32_t)row_ptr.size() - 1;
   const int kXcd = 8;
-  const double overhead = 2.0;
   std::vector<int32_t> len(nq);
   for (int32_t i = 0; i < nq; i++) len[i] = row_ptr[i + 1] - row_ptr[i];
   std::vector<int32_t> sorted_len(len);
@@ -280,7 +289,7 @@ static void build_schedule(const std::vector<int32_t>& row_ptr, int32_t heads,
   std::stable_sort(long_rows.begin(), long_rows.end(),
                    [&](int32_t a, int32_t b) { return len[a] > len[b]; });
   double long_cost = 0;
-  for (int32_t i : long_rows) long_cost += len[i] + overhead;
+  for (int32_t i : long_rows) long_cost += len[i] + kUnitOverhead;
   for (int32_t h = 0; h < heads && !long_rows.empty(); h++) {
     const int x = (int)(std::min_element(cost.begin(), cost.end()) - cost.begin());
     for (int32_t i : long_rows) lists[x].push_back(enc(h, i));
@@ -295,7 +304,7 @@ static void build_schedule(const std::vector<int32_t>& row_ptr, int32_t heads,
     for (int32_t i = 0; i < nq; i++)
       if (len[i] < long_at) {
         regular.push_back(enc(h, i));
-        reg_cost += len[i] + overhead;
+        reg_cost += len[i] + kUnitOverhead;
       }
   double total = reg_cost;
   for (double c : cost) total += c;
@@ -310,15 +319,32 @@ static void build_schedule(const std::vector<int32_t>& row_ptr, int32_t heads,
     while (pos < regular.size() && (oi == kXcd - 1 || cost[x] < target)) {
       const int32_t qt = regular[pos] & 0xffff;
       lists[x].push_back(regular[pos]);
-      cost[x] += len[qt] + overhead;
+      cost[x] += len[qt] + kUnitOverhead;
       pos++;
     }
   }
-  size_t slots = 0;
-  for (auto& l : lists) slots = std::max(slots, l.size());
-  work.assign(slots * kXcd, -1);
-  for (int x = 0; x < kXcd; x++)
-    for (size_t s = 0; s < lists[x].size(); s++) work[s * kXcd + x] = lists[x][s];
+  // Each XCD's list onto its groups / 8 workgroups (workgroup c*8 + x is the
+  // c-th of XCD x).
+  const int per_xcd = groups / kXcd;
+  std::vector<std::vector<int32_t>> per_wg(groups);
+  for (int x = 0; x < kXcd; x++) {
+    std::priority_queue<std::pair<double, int>, std::vector<std::pair<double, int>>,
+                        std::greater<std::pair<double, int>>>
+        free_at;
+    for (int c = 0; c < per_xcd; c++) free_at.push({0.0, c});
+    for (int32_t u : lists[x]) {
+      const auto [t, c] = free_at.top();
+      free_at.pop();
+      per_wg[c * kXcd + x].push_back(u);
+      free_at.push({t + len[u & 0xffff] + kUnitOverhead, c});
+    }
+  }
+  work_ptr.assign(groups + 1, 0);
+  work.clear();
+  for (int b = 0; b < groups; b++) {
+    work.insert(work.end(), per_wg[b].begin(), per_wg[b].end());
+    work_ptr[b + 1] = (int32_t)work.size();
+  }
 }
 
 static int csr_on_device(const uint8_t* d_bitmap, int32_t nq, int32_t nk, int32_t* d_row_ptr,
@@ -441,13 +467,25 @@ int h3hip_plan_create(const h3hip_mask_rule* rule, int32_t heads, const h3hip_po
   (void)hipFree(d_bitmap);
   d_bitmap = nullptr;
 
-  build_schedule(p->row_ptr, heads, p->work);
-  if (hipMalloc(&p->d_work, sizeof(int32_t) * p->work.size()) != hipSuccess) {
+  // One persistent attention workgroup per CU, a whole number per XCD.
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    set_error("querying the device's CU count failed");
+    return fail(H3HIP_EHIP);
+  }
+  p->groups = std::max(8, cus / 8 * 8);
+  build_schedule(p->row_ptr, heads, p->groups, p->work_ptr, p->work);
+  if (hipMalloc(&p->d_work_ptr, sizeof(int32_t) * p->work_ptr.size()) != hipSuccess ||
+      hipMalloc(&p->d_work, sizeof(int32_t) * std::max<size_t>(p->work.size(), 1)) != hipSuccess) {
     set_error("device allocation for the work list failed");
     return fail(H3HIP_ENOMEM);
   }
-  if (hipMemcpyAsync(p->d_work, p->work.data(), sizeof(int32_t) * p->work.size(),
+  if (hipMemcpyAsync(p->d_work_ptr, p->work_ptr.data(), sizeof(int32_t) * p->work_ptr.size(),
                      hipMemcpyHostToDevice, s) != hipSuccess ||
+      (!p->work.empty() &&
+       hipMemcpyAsync(p->d_work, p->work.data(), sizeof(int32_t) * p->work.size(),
+                      hipMemcpyHostToDevice, s) != hipSuccess) ||
       hipStreamSynchronize(s) != hipSuccess) {
     set_error("uploading the work list failed");
     return fail(H3HIP_EHIP);
@@ -461,6 +499,7 @@ int h3hip_plan_destroy(h3hip_plan p) {
   if (p->d_row_ptr) (void)hipFree(p->d_row_ptr);
   if (p->d_col_idx) (void)hipFree(p->d_col_idx);
   if (p->d_work) (void)hipFree(p->d_work);
+  if (p->d_work_ptr) (void)hipFree(p->d_work_ptr);
   delete p;
   return H3HIP_OK;
 }

@@ -129,7 +129,8 @@ class Policy:
 
 class TilePlan:
     """Owns an ``h3hip_plan``: CSR tile lists on host and device plus the
-    XCD-aware launch order, built on the current GPU."""
+    attention kernel's XCD-aware schedule (each persistent workgroup's units),
+    built on the current GPU."""
 
     def __init__(self, rule: MaskRule, heads: int, policy: Policy | None = None,
                  stream: int | None = None):

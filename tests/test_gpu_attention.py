@@ -97,6 +97,35 @@ def test_bitmap_with_empty_rows_gives_zero_rows(h3, orc):
     assert mx < MAX_ABS and mean < MEAN_ABS
 
 
+def test_many_units_per_workgroup_mixed_rows(h3, orc):
+    """1,024 units (16 heads x 64 query tiles) on the persistent workgroups,
+    several per workgroup: empty rows, a full row, a ragged last tile and rows
+    of every length follow one another in each workgroup's list, so every
+    unit's state and its first K/Q tiles must start clean. Three heads are
+    checked on every row."""
+    note("many units per workgroup")
+    rng = np.random.default_rng(11)
+    n, H = 64, 16
+    bm = (rng.random((n, n)) < 0.2).astype(np.uint8)
+    bm[[5, 6, 30, 63]] = 0
+    bm[10] = 1
+    bm[np.arange(n), np.arange(n)] |= (rng.random(n) < 0.5).astype(np.uint8)
+    bm[[5, 6, 30, 63]] = 0
+    plan, q, k, v, out, scale = run_plan(h3, h3.MaskRule.from_bitmap(n * 128 - 37, bm), H, seed=12)
+    S = plan.seq_len
+    o = f32(out)
+    assert np.all(np.isfinite(o)) and np.all(o[:, S:] == 0)
+    for t in (5, 6, 30):
+        assert np.all(o[:, t * 128:(t + 1) * 128] == 0)
+    assert np.all(o[:, 63 * 128:S] == 0)
+    rows = np.arange(S, dtype=np.int32)
+    for h in (0, 7, 15):
+        want = orc.attend_rows(f32(q[h])[rows], rows, f32(k[h, :S]), f32(v[h, :S]), scale, bm,
+                               tile=128)
+        mx, mean = err_stats(o[h, :S], want)
+        assert mx < MAX_ABS and mean < MEAN_ABS, (h, mx, mean)
+
+
 def test_token_major_output_and_determinism(h3):
     from h3hip import configs as C, ops
     note("layouts + determinism")
