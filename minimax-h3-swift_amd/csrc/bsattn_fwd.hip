@@ -23,8 +23,9 @@
 // are rescaled by 2^(m - m_new) when the running max moves. The rescale is
 // lazy: m is only raised when a tile's max exceeds it by more than 2^8, which
 // keeps every exponentiated score <= 256 and changes nothing in exact
-// arithmetic (numerator and denominator share m). The output is
-// O / max(l, 1e-30).
+// arithmetic (numerator and denominator share m). l sums the bf16-rounded
+// weights that O accumulates, so both sides of the quotient see the same
+// weights. The output is O / max(l, 1e-30).
 #include <cmath>
 
 #include "common.h"
@@ -327,21 +328,27 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; r++) oacc[db][r] *= alpha;
     }
-    float psum = 0.f;
 #pragma unroll
     for (int b = 0; b < 2; b++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(sacc[b][r], c, -m));
-        sacc[b][r] = e;
-        psum += e;
-      }
-    l += psum;
+      for (int r = 0; r < 16; r++) sacc[b][r] = __builtin_amdgcn_exp2f(fmaf(sacc[b][r], c, -m));
     // Chunk kc of P^T: registers 8*(kc&1) .. +7 of block kc>>1; element e of
     // half-wave hh is key 16kc + 8(e/4) + 4hh + e%4, matching the rows the
     // two transpose loads of the V^T operand fetch.
 #pragma unroll
     for (int kc = 0; kc < 4; kc++) pb[kc] = to_bf16x8(sacc[kc >> 1], 8 * (kc & 1));
+    // The row sum of the bf16 P that O accumulates: pairs dotted with (1, 1),
+    // so numerator and denominator use the same rounded weights.
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    float ps[2] = {0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < 4; kc++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        ps[kc & 1] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pb[kc][2 * i], pb[kc][2 * i + 1]},
+                                                     ones, ps[kc & 1], false);
+    l += ps[0] + ps[1];
   };
 
   if (n > 0) {
