@@ -168,278 +168,279 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
   const int u_beg = a.work_ptr[blockIdx.x], u_end = a.work_ptr[blockIdx.x + 1];
   if (half == 1 && u_beg < u_end) load_unit_start(a, lds, a.work[u_beg], qg, threadIdx.x & 63);
   for (int iu = u_beg; iu < u_end; iu++) {
-  // Lane-derived offsets are rebuilt for each unit from an opaque copy of the
-  // thread index: hoisted out of the unit loop they would hold registers that
-  // the operand pipelines of the inner loops need.
-  int tid;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(threadIdx.x));
-  const int lane = tid & 63;
-  const int li = lane & 31, hh = lane >> 5;
-  // K operand offsets: block b row half*64 + 32b + li, chunk 2s + hh.
-  int k_off[8];
+    // Lane-derived offsets are rebuilt for each unit from an opaque copy of the
+    // thread index: hoisted out of the unit loop they would hold registers that
+    // the operand pipelines of the inner loops need.
+    int tid;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(threadIdx.x));
+    const int lane = tid & 63;
+    const int li = lane & 31, hh = lane >> 5;
+    // K operand offsets: block b row half*64 + 32b + li, chunk 2s + hh.
+    int k_off[8];
 #pragma unroll
-  for (int s = 0; s < 8; s++) k_off[s] = (half * 64 + li) * kD + (((2 * s + hh) ^ k_swz(li)) * 8);
-  // V^T operand offsets: lane (g = lane/16, m = lane%16) points at row
-  // half*64 + 16kc + 8p + 4(g/2) + m/4, element 32db + 16(g%2) + 4(m%4).
-  const int g = lane >> 4, mm = lane & 15;
-  int v_off[2][4];
+    for (int s = 0; s < 8; s++) k_off[s] = (half * 64 + li) * kD + (((2 * s + hh) ^ k_swz(li)) * 8);
+    // V^T operand offsets: lane (g = lane/16, m = lane%16) points at row
+    // half*64 + 16kc + 8p + 4(g/2) + m/4, element 32db + 16(g%2) + 4(m%4).
+    const int g = lane >> 4, mm = lane & 15;
+    int v_off[2][4];
 #pragma unroll
-  for (int p = 0; p < 2; p++)
+    for (int p = 0; p < 2; p++)
 #pragma unroll
-    for (int db = 0; db < 4; db++) {
-      const int row = half * 64 + 8 * p + 4 * (g >> 1) + (mm >> 2);
-      const int chunk = 4 * db + 2 * (g & 1) + ((mm & 3) >> 1);
-      v_off[p][db] = row * kD + ((chunk ^ v_swz(row)) * 8) + 4 * (mm & 1);
+      for (int db = 0; db < 4; db++) {
+        const int row = half * 64 + 8 * p + 4 * (g >> 1) + (mm >> 2);
+        const int chunk = 4 * db + 2 * (g & 1) + ((mm & 3) >> 1);
+        v_off[p][db] = row * kD + ((chunk ^ v_swz(row)) * 8) + 4 * (mm & 1);
+      }
+    const int dma_row = 32 * qg + (lane >> 4);
+
+    const int32_t unit = a.work[iu];
+    const int head = unit >> 16, qt = unit & 0xffff;
+    const int q0 = qt * kTile + qg * 32;
+
+    // The unit's K(0) and Q have landed (the loading waves wait for their own
+    // loads), and the previous unit's merge buffers have been read.
+    if (half == 1) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+
+    // Q^T as the B operand, from the Q slot: lane (li, hh) holds
+    // Q[q0 + li][16s + 8hh .. +7]; query rows past seq_len are zero.
+    bf16x8 qreg[8];
+    {
+      const bool q_valid = q0 + li < a.seq_len;
+      const uint16_t* qrow = lds + 4 * kSlot + (qg * 32 + li) * kD;
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+        const bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + (((2 * s + hh) ^ k_swz(li)) * 8));
+        qreg[s] = q_valid ? x : bf16x8{};
+      }
     }
-  const int dma_row = 32 * qg + (lane >> 4);
 
-  const int32_t unit = a.work[iu];
-  const int head = unit >> 16, qt = unit & 0xffff;
-  const int q0 = qt * kTile + qg * 32;
-
-  // The unit's K(0) and Q have landed (the loading waves wait for their own
-  // loads), and the previous unit's merge buffers have been read.
-  if (half == 1) __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  __syncthreads();
-
-  // Q^T as the B operand, from the Q slot: lane (li, hh) holds
-  // Q[q0 + li][16s + 8hh .. +7]; query rows past seq_len are zero.
-  bf16x8 qreg[8];
-  {
-    const bool q_valid = q0 + li < a.seq_len;
-    const uint16_t* qrow = lds + 4 * kSlot + (qg * 32 + li) * kD;
+    // HBM -> LDS by one half of the workgroup, as buffer loads (a per-head
+    // resource bounded at row seq_len, 32-bit lane offsets): wave w moves rows
+    // 32(w&3) .. +31 of a tile, 4 rows per instruction; lane l fills chunk
+    // position l%16 of row 32(w&3) + 4i + l/16 from the global chunk that the
+    // swizzle places there. The whole offset is in the lane offset, which the
+    // hardware range-checks, so rows at or past seq_len are never fetched.
+    const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.k + head * a.k_hs), 0, (a.seq_len - 1) * k_rs2 + kD * 2, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.v + head * a.v_hs), 0, (a.seq_len - 1) * v_rs2 + kD * 2, kBufferWord3);
+    auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int key0, uint16_t* slot,
+                   bool v_layout) __attribute__((always_inline)) {
+      const int rs2 = v_layout ? v_rs2 : k_rs2;
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
-      const bf16x8 x = *reinterpret_cast<const bf16x8*>(qrow + (((2 * s + hh) ^ k_swz(li)) * 8));
-      qreg[s] = q_valid ? x : bf16x8{};
-    }
-  }
+      for (int i = 0; i < 8; i++) {
+        const int row = dma_row + 4 * i;
+        const int swz = v_layout ? v_swz(row) : k_swz(row);
+        const int voff = (key0 + row) * rs2 + (((lane & 15) ^ swz) * 16);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsrc, (lds_void*)(slot + (32 * qg + 4 * i) * kD), 16, voff, 0, 0, 0);
+      }
+    };
 
-  // HBM -> LDS by one half of the workgroup, as buffer loads (a per-head
-  // resource bounded at row seq_len, 32-bit lane offsets): wave w moves rows
-  // 32(w&3) .. +31 of a tile, 4 rows per instruction; lane l fills chunk
-  // position l%16 of row 32(w&3) + 4i + l/16 from the global chunk that the
-  // swizzle places there. The whole offset is in the lane offset, which the
-  // hardware range-checks, so rows at or past seq_len are never fetched.
-  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.k + head * a.k_hs), 0, (a.seq_len - 1) * k_rs2 + kD * 2, kBufferWord3);
-  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.v + head * a.v_hs), 0, (a.seq_len - 1) * v_rs2 + kD * 2, kBufferWord3);
-  auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int key0, uint16_t* slot,
-                 bool v_layout) __attribute__((always_inline)) {
-    const int rs2 = v_layout ? v_rs2 : k_rs2;
+    f32x16 oacc[4];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int row = dma_row + 4 * i;
-      const int swz = v_layout ? v_swz(row) : k_swz(row);
-      const int voff = (key0 + row) * rs2 + (((lane & 15) ^ swz) * 16);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rsrc, (lds_void*)(slot + (32 * qg + 4 * i) * kD), 16, voff, 0, 0, 0);
-    }
-  };
-
-  f32x16 oacc[4];
+    for (int db = 0; db < 4; db++)
 #pragma unroll
-  for (int db = 0; db < 4; db++)
+      for (int r = 0; r < 16; r++) oacc[db][r] = 0.f;
+    float m = -3.0e38f, l = 0.f;
+    f32x16 sacc[2];
+    bf16x8 pb[4];
+
+    const int beg = a.row_ptr[qt], n = a.row_ptr[qt + 1] - beg;
+    // Column indices through the constant address space: scalar loads.
+    const __attribute__((address_space(4))) int32_t* cols =
+        (const __attribute__((address_space(4))) int32_t*)(a.col_idx) + beg;
+
+    // M_j: S(j) = K(j) Q^T and O += V(j-1)^T P(j-1).
+    auto m_phase = [&](int j) __attribute__((always_inline)) {
+      if (j < n) {
+        const uint16_t* kb = lds + (j & 1) * kSlot;
 #pragma unroll
-    for (int r = 0; r < 16; r++) oacc[db][r] = 0.f;
-  float m = -3.0e38f, l = 0.f;
-  f32x16 sacc[2];
-  bf16x8 pb[4];
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) sacc[b][r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+#pragma unroll
+          for (int b = 0; b < 2; b++) {
+            const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kb + k_off[s] + b * 32 * kD);
+            sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[s], sacc[b], 0, 0, 0);
+          }
+        }
+        // Operand reads run four MFMAs ahead of their use.
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 12; i++) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+      }
+      if (j >= 1) {
+        const uint16_t* vb = lds + (2 + ((j - 1) & 1)) * kSlot;
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++)
+#pragma unroll
+          for (int db = 0; db < 4; db++) {
+            const bf16x8 va = vt_operand(vb + v_off[0][db] + 16 * kc * kD,
+                                         vb + v_off[1][db] + 16 * kc * kD);
+            oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kc], oacc[db], 0, 0, 0);
+          }
+        // Each V^T operand is two transpose reads; keep four operands in flight.
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+#pragma unroll
+        for (int i = 0; i < 12; i++) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+      }
+    };
 
-  const int beg = a.row_ptr[qt], n = a.row_ptr[qt + 1] - beg;
-  // Column indices through the constant address space: scalar loads.
-  const __attribute__((address_space(4))) int32_t* cols =
-      (const __attribute__((address_space(4))) int32_t*)(a.col_idx) + beg;
-
-  // M_j: S(j) = K(j) Q^T and O += V(j-1)^T P(j-1).
-  auto m_phase = [&](int j) __attribute__((always_inline)) {
-    if (j < n) {
-      const uint16_t* kb = lds + (j & 1) * kSlot;
+    // V_j: online softmax of S(j) into P(j) (bf16 B operands).
+    auto v_phase = [&](int j) __attribute__((always_inline)) {
+      const int key0 = cols[j] * kTile;
+      if (key0 + kTile > a.seq_len) {
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const int key = key0 + half * 64 + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
+            if (key >= a.seq_len) sacc[b][r] = -1.0e30f;
+          }
+      }
+      float mx = -3.0e38f;
 #pragma unroll
       for (int b = 0; b < 2; b++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) sacc[b][r] = 0.f;
+        for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[b][r]);
+      mx = max_xor32(mx);
+      const float m_cand = fmaxf(m, mx * c);
+      const bool raise = m_cand > m + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+        const float m_new = raise ? m_cand : m;
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        m = m_new;
+        l *= alpha;
 #pragma unroll
-      for (int s = 0; s < 8; s++) {
+        for (int db = 0; db < 4; db++)
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-          const bf16x8 ka = *reinterpret_cast<const bf16x8*>(kb + k_off[s] + b * 32 * kD);
-          sacc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qreg[s], sacc[b], 0, 0, 0);
-        }
+          for (int r = 0; r < 16; r++) oacc[db][r] *= alpha;
       }
-      // Operand reads run four MFMAs ahead of their use.
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
-      for (int i = 0; i < 12; i++) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
-    }
-    if (j >= 1) {
-      const uint16_t* vb = lds + (2 + ((j - 1) & 1)) * kSlot;
+      for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) sacc[b][r] = __builtin_amdgcn_exp2f(fmaf(sacc[b][r], c, -m));
+      // Chunk kc of P^T: registers 8*(kc&1) .. +7 of block kc>>1; element e of
+      // half-wave hh is key 16kc + 8(e/4) + 4hh + e%4, matching the rows the
+      // two transpose loads of the V^T operand fetch.
+#pragma unroll
+      for (int kc = 0; kc < 4; kc++) pb[kc] = to_bf16x8(sacc[kc >> 1], 8 * (kc & 1));
+      // The row sum of the bf16 P that O accumulates: pairs dotted with (1, 1),
+      // so numerator and denominator use the same rounded weights.
+      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+      const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+      float ps[2] = {0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; kc++)
 #pragma unroll
-        for (int db = 0; db < 4; db++) {
-          const bf16x8 va = vt_operand(vb + v_off[0][db] + 16 * kc * kD,
-                                       vb + v_off[1][db] + 16 * kc * kD);
-          oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kc], oacc[db], 0, 0, 0);
-        }
-      // Each V^T operand is two transpose reads; keep four operands in flight.
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
-#pragma unroll
-      for (int i = 0; i < 12; i++) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
-    }
-  };
+        for (int i = 0; i < 4; i++)
+          ps[kc & 1] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pb[kc][2 * i], pb[kc][2 * i + 1]},
+                                                       ones, ps[kc & 1], false);
+      l += ps[0] + ps[1];
+    };
 
-  // V_j: online softmax of S(j) into P(j) (bf16 B operands).
-  auto v_phase = [&](int j) __attribute__((always_inline)) {
-    const int key0 = cols[j] * kTile;
-    if (key0 + kTile > a.seq_len) {
+    if (n > 0) {
+      // Each half runs its own loop of two phases per tile (2n + 2 phases and
+      // barriers in all), so neither loop merges the other role's state.
+      if (half == 0) {
+        for (int j = 0; j <= n; j++) {
+          m_phase(j);                                       // phase 2j
+          __syncthreads();
+          if (j < n) {                                      // phase 2j + 1
+            const int key0 = cols[j] * kTile;
+            uint16_t* vb = lds + (2 + (j & 1)) * kSlot;
+            dma(v_rsrc, key0, vb, true);
+            v_phase(j);
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            // Rows past seq_len of a ragged tile are zeroed after they land, so
+            // padding never reaches P V (0 * NaN would).
+            if (key0 + kTile > a.seq_len) {
 #pragma unroll
-      for (int b = 0; b < 2; b++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int key = key0 + half * 64 + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key >= a.seq_len) sacc[b][r] = -1.0e30f;
+              for (int i = 0; i < 8; i++) {
+                const int row = dma_row + 4 * i;
+                if (key0 + row >= a.seq_len)
+                  *reinterpret_cast<u32x4*>(vb + row * kD + (lane & 15) * 8) =
+                      u32x4{0u, 0u, 0u, 0u};
+              }
+            }
+          }
+          __syncthreads();
         }
+      } else {
+        for (int j = 0; j <= n; j++) {
+          if (j + 1 < n) dma(k_rsrc, cols[j + 1] * kTile, lds + ((j + 1) & 1) * kSlot, false);
+          if (j >= 1) v_phase(j - 1);                       // phase 2j
+          __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+          __syncthreads();
+          m_phase(j);                                       // phase 2j + 1
+          __syncthreads();
+        }
+      }
     }
-    float mx = -3.0e38f;
-#pragma unroll
-    for (int b = 0; b < 2; b++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) mx = fmaxf(mx, sacc[b][r]);
-    mx = max_xor32(mx);
-    const float m_cand = fmaxf(m, mx * c);
-    const bool raise = m_cand > m + kRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-      const float m_new = raise ? m_cand : m;
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-      m = m_new;
-      l *= alpha;
+
+    // Merge the two key halves of each query (exact: rescale both to the larger
+    // m). Waves 4-7 leave (O, m, l) in LDS -- O in the two V slots, m and l in
+    // K slot 1 -- then, while waves 0-3 merge and store, start the next unit's
+    // K(0) and Q loads into K slot 0 and the Q slot, which no wave reads any
+    // more in this unit.
+    const float lt = l + __shfl_xor(l, 32);
+    float* xo = reinterpret_cast<float*>(lds + 2 * kSlot) + qg * 64 * 64;
+    float* xm = reinterpret_cast<float*>(lds + kSlot);
+    float* xl = xm + 4 * 64;
+    if (half == 1) {
 #pragma unroll
       for (int db = 0; db < 4; db++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) oacc[db][r] *= alpha;
+        for (int r = 0; r < 16; r++) xo[(db * 16 + r) * 64 + lane] = oacc[db][r];
+      xm[qg * 64 + lane] = m;
+      xl[qg * 64 + lane] = lt;
     }
-#pragma unroll
-    for (int b = 0; b < 2; b++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) sacc[b][r] = __builtin_amdgcn_exp2f(fmaf(sacc[b][r], c, -m));
-    // Chunk kc of P^T: registers 8*(kc&1) .. +7 of block kc>>1; element e of
-    // half-wave hh is key 16kc + 8(e/4) + 4hh + e%4, matching the rows the
-    // two transpose loads of the V^T operand fetch.
-#pragma unroll
-    for (int kc = 0; kc < 4; kc++) pb[kc] = to_bf16x8(sacc[kc >> 1], 8 * (kc & 1));
-    // The row sum of the bf16 P that O accumulates: pairs dotted with (1, 1),
-    // so numerator and denominator use the same rounded weights.
-    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-    float ps[2] = {0.f, 0.f};
-#pragma unroll
-    for (int kc = 0; kc < 4; kc++)
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        ps[kc & 1] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{pb[kc][2 * i], pb[kc][2 * i + 1]},
-                                                     ones, ps[kc & 1], false);
-    l += ps[0] + ps[1];
-  };
-
-  if (n > 0) {
-    // Each half runs its own loop of two phases per tile (2n + 2 phases and
-    // barriers in all), so neither loop merges the other role's state.
+    __syncthreads();
+    if (half == 1 && iu + 1 < u_end) load_unit_start(a, lds, a.work[iu + 1], qg, lane);
     if (half == 0) {
-      for (int j = 0; j <= n; j++) {
-        m_phase(j);                                       // phase 2j
-        __syncthreads();
-        if (j < n) {                                      // phase 2j + 1
-          const int key0 = cols[j] * kTile;
-          uint16_t* vb = lds + (2 + (j & 1)) * kSlot;
-          dma(v_rsrc, key0, vb, true);
-          v_phase(j);
-          __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-          // Rows past seq_len of a ragged tile are zeroed after they land, so
-          // padding never reaches P V (0 * NaN would).
-          if (key0 + kTile > a.seq_len) {
+    const float m1 = xm[qg * 64 + lane], l1 = xl[qg * 64 + lane];
+    const float mmax = fmaxf(m, m1);
+    const float f0 = __builtin_amdgcn_exp2f(m - mmax), f1 = __builtin_amdgcn_exp2f(m1 - mmax);
+    const float inv = 1.0f / fmaxf(lt * f0 + l1 * f1, 1.0e-30f);
+    const float s0 = f0 * inv, s1 = f1 * inv;
+
+    // O^T C layout: lane (li, hh) holds query q0 + li, channels
+    // 32db + 8g + 4hh + [0, 4) in registers 4g .. 4g + 3.
+    const int qi = q0 + li;
+    const bool valid = qi < a.seq_len;
+    if (qi < a.out_rows) {
+      uint16_t* orow = a.out + head * a.o_hs + (int64_t)qi * a.o_rs;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-              const int row = dma_row + 4 * i;
-              if (key0 + row >= a.seq_len)
-                *reinterpret_cast<u32x4*>(vb + row * kD + (lane & 15) * 8) = u32x4{0u, 0u, 0u, 0u};
-            }
+      for (int db = 0; db < 4; db++)
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) {
+          float o[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int r = 4 * gg + e;
+            o[e] = oacc[db][r] * s0 + xo[(db * 16 + r) * 64 + lane] * s1;
           }
+          u32x2 w = {0u, 0u};
+          if (valid) {
+            w[0] = pack_bf16x2(o[0], o[1]);
+            w[1] = pack_bf16x2(o[2], o[3]);
+          }
+          *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * gg + 4 * hh) = w;
         }
-        __syncthreads();
-      }
-    } else {
-      for (int j = 0; j <= n; j++) {
-        if (j + 1 < n) dma(k_rsrc, cols[j + 1] * kTile, lds + ((j + 1) & 1) * kSlot, false);
-        if (j >= 1) v_phase(j - 1);                       // phase 2j
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        __syncthreads();
-        m_phase(j);                                       // phase 2j + 1
-        __syncthreads();
-      }
     }
-  }
-
-  // Merge the two key halves of each query (exact: rescale both to the larger
-  // m). Waves 4-7 leave (O, m, l) in LDS -- O in the two V slots, m and l in
-  // K slot 1 -- then, while waves 0-3 merge and store, start the next unit's
-  // K(0) and Q loads into K slot 0 and the Q slot, which no wave reads any
-  // more in this unit.
-  const float lt = l + __shfl_xor(l, 32);
-  float* xo = reinterpret_cast<float*>(lds + 2 * kSlot) + qg * 64 * 64;
-  float* xm = reinterpret_cast<float*>(lds + kSlot);
-  float* xl = xm + 4 * 64;
-  if (half == 1) {
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) xo[(db * 16 + r) * 64 + lane] = oacc[db][r];
-    xm[qg * 64 + lane] = m;
-    xl[qg * 64 + lane] = lt;
-  }
-  __syncthreads();
-  if (half == 1 && iu + 1 < u_end) load_unit_start(a, lds, a.work[iu + 1], qg, lane);
-  if (half == 0) {
-  const float m1 = xm[qg * 64 + lane], l1 = xl[qg * 64 + lane];
-  const float mmax = fmaxf(m, m1);
-  const float f0 = __builtin_amdgcn_exp2f(m - mmax), f1 = __builtin_amdgcn_exp2f(m1 - mmax);
-  const float inv = 1.0f / fmaxf(lt * f0 + l1 * f1, 1.0e-30f);
-  const float s0 = f0 * inv, s1 = f1 * inv;
-
-  // O^T C layout: lane (li, hh) holds query q0 + li, channels
-  // 32db + 8g + 4hh + [0, 4) in registers 4g .. 4g + 3.
-  const int qi = q0 + li;
-  const bool valid = qi < a.seq_len;
-  if (qi < a.out_rows) {
-    uint16_t* orow = a.out + head * a.o_hs + (int64_t)qi * a.o_rs;
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-      for (int gg = 0; gg < 4; gg++) {
-        float o[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int r = 4 * gg + e;
-          o[e] = oacc[db][r] * s0 + xo[(db * 16 + r) * 64 + lane] * s1;
-        }
-        u32x2 w = {0u, 0u};
-        if (valid) {
-          w[0] = pack_bf16x2(o[0], o[1]);
-          w[1] = pack_bf16x2(o[2], o[3]);
-        }
-        *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * gg + 4 * hh) = w;
-      }
-  }
-  }
+    }
   }
 }
 
