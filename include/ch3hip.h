@@ -137,6 +137,18 @@ int h3hip_plan_tiles(h3hip_plan plan, int32_t* row_ptr, int32_t* col_idx);
  * (AxialTopology.swift:139-170), counted on tiles. */
 double h3hip_plan_density(h3hip_plan plan);
 
+/* The attention launch's persistent schedule for a plan with these CSR rows
+ * (host-side, synchronous; h3hip_plan_create builds the same lists). No
+ * counterpart in the reference, whose MLX dispatch has no persistent
+ * workgroups; exposed so callers and tests can inspect which (head, q-tile)
+ * units each workgroup runs. row_ptr[n_tiles + 1]; groups = workgroups, a
+ * positive multiple of 8 (one per CU: 256 on MI355X). Writes
+ * work_ptr[groups + 1] and work[heads * n_tiles]: workgroup b runs units
+ * work[work_ptr[b] .. work_ptr[b + 1]) in order, each (head << 16 | q_tile),
+ * every unit exactly once. */
+int h3hip_schedule(const int32_t* row_ptr, int32_t n_tiles, int32_t heads, int32_t groups,
+                   int32_t* work_ptr, int32_t* work);
+
 /* ------------------------------------------------------- tile-list builder */
 
 /* Device tile bitmap from a token-level rule: d_bitmap [n_tiles * n_tiles]

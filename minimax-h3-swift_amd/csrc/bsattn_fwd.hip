@@ -19,11 +19,17 @@
 //
 // The softmax is the online recurrence of AxialReference.attendStreamingKeys
 // (Sources/H3Attention/AxialReference.swift:129-171) in fp32 and base 2:
-// m starts at -3e38, keys >= seq_len take the -1e30 sentinel, and l and O
-// are rescaled by 2^(m - m_new) when the running max moves. The rescale is
-// lazy: m is only raised when a tile's max exceeds it by more than 2^8, which
-// keeps every exponentiated score <= 256 and changes nothing in exact
-// arithmetic (numerator and denominator share m). l sums the bf16-rounded
+// m starts at -3e38 and l and O are rescaled by 2^(m - m_new) when the
+// running max moves. Padding keys (>= seq_len, which the reference's unpadded
+// arrays do not have) score -inf, not the reference's finite -1e30 mask
+// sentinel: their weight is then exactly 0 whatever m is, and a 64-key half
+// made only of padding leaves m where it was. (With a finite sentinel that
+// half would raise m to round(-1e30 * c), and 2^(-1e30 * c - m) is 2 to the
+// power of the product's rounding residual, which can be +1e21: an infinite
+// weight times a zeroed V row is NaN.)
+// The rescale is lazy: m is only raised when a tile's max exceeds it by more
+// than 2^8, which keeps every exponentiated score <= 256 and changes nothing
+// in exact arithmetic (numerator and denominator share m). l sums the bf16-rounded
 // weights that O accumulates, so both sides of the quotient see the same
 // weights. The output is O / max(l, 1e-30).
 #include <cmath>
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
 #pragma unroll
           for (int r = 0; r < 16; r++) {
             const int key = key0 + half * 64 + 32 * b + 8 * (r >> 2) + 4 * hh + (r & 3);
-            if (key >= a.seq_len) sacc[b][r] = -1.0e30f;
+            if (key >= a.seq_len) sacc[b][r] = -__builtin_inff();
           }
       }
       float mx = -3.0e38f;

@@ -29,3 +29,17 @@ struct h3hip_plan_s {
   int32_t* d_work_ptr = nullptr;
   int32_t* d_work = nullptr;
 };
+
+namespace h3hip {
+
+// Thread-local last error (defined with the plan code); the ABI is re-entrant
+// per thread.
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// The persistent attention schedule for these CSR rows (schedule.cpp):
+// work_ptr[groups + 1] and work[heads * n_tiles], each unit (head << 16 |
+// q_tile) listed once. H3HIP_OK, or an error with the message set.
+int build_schedule(const std::vector<int32_t>& row_ptr, int32_t heads, int32_t groups,
+                   std::vector<int32_t>& work_ptr, std::vector<int32_t>& work);
+
+}  // namespace h3hip

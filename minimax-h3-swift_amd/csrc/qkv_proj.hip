@@ -411,6 +411,10 @@ extern "C" int h3hip_qkv_proj(const void* x, int64_t ldx, const void* w, int64_t
                               float eps, const void* rope_table, int32_t rot, int32_t rounding,
                               int32_t seq_len, int32_t seq_pad, int32_t heads, int32_t head_dim,
                               void* q_out, void* k_out, void* v_out, void* stream) {
+  // hidden <= 0 is an invalid shape, not an unsupported one (0 and negative
+  // multiples of 64 would pass the decline test below, and a negative hidden
+  // wraps the x buffer's byte range).
+  H3_REQUIRE(hidden > 0, H3HIP_EINVAL, "hidden must be positive (got %d)", hidden);
   if (head_dim != kHD || (rot != 96 && rot != 128) || heads % 2 != 0 || hidden % kPK != 0) {
     set_error("declined: head_dim %d / rot %d / heads %d / hidden %d (needs head_dim 128, rot 96 "
               "or 128, an even head count, hidden a multiple of 64)",

@@ -210,21 +210,45 @@ def qkv_proj(x: torch.Tensor, w: torch.Tensor, q_gamma: torch.Tensor | None = No
 
 # -------------------------------------------------------------------- attention
 
+def _head_major_qkv(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    """q, k, v must be contiguous bf16 GPU tensors of one shape [H, seq_pad, D]:
+    the kernel reads all H heads x D columns x seq_len rows of each. Returns (H, D).
+    (A head count or head_dim the library does not take is declined by the library
+    before anything is read.)"""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not t.is_contiguous() or t.dim() != 3 or t.shape[1] != plan.seq_pad:
+            raise ValueError(f"{name} must be contiguous [heads, {plan.seq_pad}, head_dim], "
+                             f"got shape {tuple(t.shape)}")
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k and v must have one shape, got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require_gpu_bf16(name, t)
+    return q.shape[0], q.shape[2]
+
+
+def _require_out(out: torch.Tensor, shape, device):
+    if (not isinstance(out, torch.Tensor) or out.dtype != torch.bfloat16 or out.device != device
+            or not out.is_contiguous() or tuple(out.shape) != tuple(shape)):
+        raise ValueError(f"out must be a contiguous bf16 tensor of shape {tuple(shape)} on "
+                         f"{device}, got {getattr(out, 'shape', None)}")
+
+
 def bsattn_fwd(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                scale: float | None = None, out_layout: int = L.OUT_HEAD_MAJOR,
                out: torch.Tensor | None = None):
     """Block-sparse attention over the plan's tiles; q/k/v [H, seq_pad, D] bf16.
 
     Returns the output tensor, or None when the call is declined."""
-    for name, t in (("q", q), ("k", k), ("v", v)):
-        _require_gpu_bf16(name, t)
-        if not t.is_contiguous() or t.dim() != 3 or t.shape[1] != plan.seq_pad:
-            raise ValueError(f"{name} must be contiguous [heads, {plan.seq_pad}, head_dim]")
-    H, _, D = q.shape
+    H, D = _head_major_qkv(plan, q, k, v)
     scale = 1.0 / math.sqrt(D) if scale is None else scale
+    if out_layout not in (L.OUT_HEAD_MAJOR, L.OUT_TOKEN_MAJOR):
+        raise ValueError(f"unknown out_layout {out_layout}")
+    shape = (H, plan.seq_pad, D) if out_layout == L.OUT_HEAD_MAJOR else (plan.seq_pad, H * D)
     if out is None:
-        shape = (H, plan.seq_pad, D) if out_layout == L.OUT_HEAD_MAJOR else (plan.seq_pad, H * D)
         out = torch.empty(shape, dtype=torch.bfloat16, device=q.device)
+    else:
+        _require_out(out, shape, q.device)
     rc = L.lib().h3hip_bsattn_fwd(plan.handle, _ptr(q), _ptr(k), _ptr(v), H, D, scale,
                                   _ptr(out), out_layout, _stream(q))
     if L.check(rc, allow_declined=True) == L.DECLINED:
@@ -232,13 +256,22 @@ def bsattn_fwd(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     return out
 
 
-def _view(name: str, t: torch.Tensor, min_rows: int) -> L.ViewC:
-    """[heads, rows, head_dim] tensor -> h3hip_view (strides in elements)."""
-    _require_gpu_bf16(name, t)
-    if t.dim() != 3 or t.stride(2) != 1 or t.shape[1] < min_rows:
-        raise ValueError(f"{name} must be a [heads, >= {min_rows}, head_dim] view with unit "
-                         f"stride along head_dim, got shape {tuple(t.shape)} strides {t.stride()}")
-    return L.ViewC(t.data_ptr(), t.stride(0), t.stride(1))
+def _views(q, k, v, out, S):
+    """[heads, rows, head_dim] tensors -> h3hip_views (strides in elements). The
+    kernel touches every head and all head_dim columns of rows < S of each, so
+    every view must hold q's head count and head_dim and at least S rows."""
+    if q.dim() != 3:
+        raise ValueError(f"q must be a [heads, rows, head_dim] view, got shape {tuple(q.shape)}")
+    H, _, D = q.shape
+    named = (("q", q), ("k", k), ("v", v), ("out", out))
+    for name, t in named:
+        if (t.dim() != 3 or t.stride(2) != 1 or t.shape[0] != H or t.shape[2] != D
+                or t.shape[1] < S):
+            raise ValueError(f"{name} must be a [{H}, >= {S}, {D}] view with unit stride along "
+                             f"head_dim, got shape {tuple(t.shape)} strides {t.stride()}")
+    for name, t in named:
+        _require_gpu_bf16(name, t)
+    return [L.ViewC(t.data_ptr(), t.stride(0), t.stride(1)) for _, t in named]
 
 
 def bsattn_fwd_strided(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -251,12 +284,14 @@ def bsattn_fwd_strided(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torc
     by default a token-major [S, heads*head_dim] tensor is allocated and
     returned. Returns None when the call is declined."""
     S = plan.seq_len
+    if q.dim() != 3:
+        raise ValueError(f"q must be a [heads, rows, head_dim] view, got shape {tuple(q.shape)}")
     H, _, D = q.shape
     ret = None
     if out is None:
         ret = torch.empty((S, H * D), dtype=torch.bfloat16, device=q.device)
         out = ret.view(S, H, D).transpose(0, 1)
-    views = [_view(n, t, S) for n, t in (("q", q), ("k", k), ("v", v), ("out", out))]
+    views = _views(q, k, v, out, S)
     scale = 1.0 / math.sqrt(D) if scale is None else scale
     rc = L.lib().h3hip_bsattn_fwd_strided(plan.handle, ctypes.byref(views[0]),
                                           ctypes.byref(views[1]), ctypes.byref(views[2]), H, D,
@@ -275,11 +310,13 @@ def attend_strided(plan: TilePlan, context, q: torch.Tensor, k: torch.Tensor,
     [S, heads*head_dim] buffer is allocated and its [heads, S, head_dim] view
     returned. Returns None when the call is declined."""
     S = plan.seq_len
+    if q.dim() != 3:
+        raise ValueError(f"q must be a [heads, rows, head_dim] view, got shape {tuple(q.shape)}")
     H, _, D = q.shape
     if out is None:
         out = torch.empty((S, H * D), dtype=torch.bfloat16, device=q.device)
         out = out.view(S, H, D).transpose(0, 1)
-    views = [_view(n, t, S) for n, t in (("q", q), ("k", k), ("v", v), ("out", out))]
+    views = _views(q, k, v, out, S)
     cctx = None if context is None else ctypes.byref(context.to_c())
     rc = L.lib().h3hip_attend_strided(plan.handle, cctx, ctypes.byref(views[0]),
                                       ctypes.byref(views[1]), ctypes.byref(views[2]), H, D,
@@ -293,12 +330,14 @@ def attend(plan: TilePlan, context, q: torch.Tensor, k: torch.Tensor, v: torch.T
            scale: float, out: torch.Tensor | None = None):
     """h3hip_attend: policy + geometry checks, then the sparse kernel.
 
-    ``context`` is an AttentionContext (or None, which declines)."""
-    for name, t in (("q", q), ("k", k), ("v", v)):
-        _require_gpu_bf16(name, t)
-    H, _, D = q.shape
+    ``context`` is an AttentionContext (or None, which declines). q, k, v are
+    contiguous [heads, seq_pad, head_dim] like bsattn_fwd's; a given ``out``
+    must be contiguous [heads, seq_pad, head_dim] bf16."""
+    H, D = _head_major_qkv(plan, q, k, v)
     if out is None:
         out = torch.empty((H, plan.seq_pad, D), dtype=torch.bfloat16, device=q.device)
+    else:
+        _require_out(out, (H, plan.seq_pad, D), q.device)
     cctx = None if context is None else ctypes.byref(context.to_c())
     rc = L.lib().h3hip_attend(plan.handle, cctx, _ptr(q), _ptr(k), _ptr(v), H, D, scale,
                               _ptr(out), _stream(q))

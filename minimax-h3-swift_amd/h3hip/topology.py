@@ -114,6 +114,21 @@ def axial_token_density(prefix_len: int, frames: int, height: int, width: int,
     return (prefix_len * s + video) / float(s * s)
 
 
+def schedule(row_ptr: np.ndarray, heads: int, groups: int = 256):
+    """The attention launch's persistent schedule for these CSR rows
+    (h3hip_schedule): (work_ptr [groups + 1], work [heads * n_tiles]) int32;
+    workgroup b runs work[work_ptr[b]:work_ptr[b + 1]], each unit
+    head << 16 | q_tile. The same lists h3hip_plan_create uploads."""
+    rp = np.ascontiguousarray(row_ptr, dtype=np.int32)
+    n = len(rp) - 1
+    work_ptr = np.zeros(groups + 1, dtype=np.int32)
+    work = np.zeros(max(heads * n, 1), dtype=np.int32)
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    L.check(L.lib().h3hip_schedule(rp.ctypes.data_as(i32p), n, heads, groups,
+                                   work_ptr.ctypes.data_as(i32p), work.ctypes.data_as(i32p)))
+    return work_ptr, work[:heads * n]
+
+
 @dataclass
 class Policy:
     """When the backend declines (AttentionContext-driven, AttentionBackend.swift:10-59)."""

@@ -118,6 +118,11 @@ def test_projection_and_rope_table_refusals(h3):
     rc = lib.h3hip_qkv_proj(buf, 128, buf, 128, 128, None, None, 1e-6, None, 128, 0, 4, 144, 2,
                             128, buf, buf, buf, None)
     assert rc == _lib.EINVAL and "seq_pad" in h3.last_error()
+    # hidden 0 or a negative multiple of 64: refused, not declined.
+    for hidden in (0, -64):
+        rc = lib.h3hip_qkv_proj(buf, 128, buf, 128, hidden, None, None, 1e-6, None, 128, 0, 4,
+                                128, 2, 128, buf, buf, buf, None)
+        assert rc == _lib.EINVAL and "hidden" in h3.last_error(), hidden
     assert lib.h3hip_rope_table(None, None, None, 128, 0, 4, None, None) == _lib.EINVAL
     rc = lib.h3hip_rope_table(buf, buf, buf, 127, 0, 4, buf, None)
     assert rc == _lib.EINVAL and "rot" in h3.last_error()
