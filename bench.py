@@ -44,6 +44,46 @@ def read_traffic(name: str):
     return None
 
 
+def interleaved_medians(fns: dict, reps: int = 12, warmup: int = 2) -> dict:
+    """Median per-call milliseconds of each callable, the calls interleaved in
+    alternating order (A B C, C B A, A B C, ...), each bracketed by HIP events on
+    the stream it launches on (torch's current stream) -- the interleaved-median
+    discipline of the reference's BenchmarkSupport.swift:10-30."""
+    import numpy as np
+    import torch
+    names = list(fns)
+    for _ in range(warmup):
+        for n in names:
+            fns[n]()
+    ev = {n: [] for n in names}
+    for r in range(reps):
+        for n in (names if r % 2 == 0 else names[::-1]):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fns[n]()
+            b.record()
+            ev[n].append((a, b))
+    torch.cuda.synchronize()
+    return {n: float(np.median([a.elapsed_time(b) for a, b in ev[n]])) for n in names}
+
+
+def host_cpu():
+    """CPU model, logical CPUs and the threads OpenMP would use on this host."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, avail, os.environ.get("OMP_NUM_THREADS")
+
+
 def cpu_baseline(shape, plan_rows, seconds: float = 12.0):
     """The reference path on the host CPU: the oracle's restatement of
     AxialReference.attend (fp32, additive -1e30 mask over all S keys) on a
@@ -61,7 +101,10 @@ def cpu_baseline(shape, plan_rows, seconds: float = 12.0):
     rng = np.random.default_rng(0)
     k = rng.standard_normal((S, D), dtype=np.float32)
     v = rng.standard_normal((S, D), dtype=np.float32)
-    threads = min(16, os.cpu_count() or 1)
+    model, nproc, avail, omp_env = host_cpu()
+    # Every host CPU this process may run on, at most the 16 that the GPU box
+    # allots to one GPU.
+    threads = min(16, avail)
 
     rows = np.arange(S, dtype=np.int32)
     q = rng.standard_normal((S, D), dtype=np.float32)
@@ -81,6 +124,10 @@ def cpu_baseline(shape, plan_rows, seconds: float = 12.0):
         "value": round(n_heads * head_flops / dt / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": threads,
+        "cpu_model": model,
+        "nproc": nproc,
+        "cpus_available": avail,
+        "omp_num_threads_env": omp_env,
         "kind": "port",
         "sample": (f"oracle dense-masked attention (AxialReference.attend restated in C, "
                    f"OpenMP, fp32, every query row scored against all {S} keys) on {n_heads} of "
@@ -170,21 +217,13 @@ def qkv_projection_extra(args, env):
         ops.qk_norm_rope(qkv_tmp[:, :inner], qkv_tmp[:, inner:2 * inner], *tables, heads=H,
                          eps=env["C"].QK_EPS, seq_pad=S_pad, out=(qh, kh, None))
 
-    reps = max(10, args.steps)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(reps + 3)]
-    for e in ev:
-        e[0].record()
-        fused()
-        e[1].record()
-        gemm()
-        e[2].record()
-        prologue()
-        e[3].record()
-    torch.cuda.synchronize()
-    t = [float(np.mean([e[i].elapsed_time(e[i + 1]) for e in ev[3:]])) for i in range(3)]
+    med = interleaved_medians({"fused": fused, "gemm": gemm, "prologue": prologue},
+                              reps=max(12, args.steps))
+    t = [med["fused"], med["gemm"], med["prologue"]]
     flops = 2.0 * S * C_HIDDEN * 3 * inner
     tf = lambda ms: round(flops / (ms * 1e-3) / 1e12, 1)
-    return {"fused_ms": round(t[0], 4), "fused_tflops": tf(t[0]),
+    return {"timing": "medians of interleaved calls", "fused_ms": round(t[0], 4),
+            "fused_tflops": tf(t[0]),
             "fused_mfma_peak_frac": round(flops / (t[0] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
             "hipblaslt_gemm_ms": round(t[1], 4), "hipblaslt_gemm_tflops": tf(t[1]),
             "prologue_after_gemm_ms": round(t[2], 4),
@@ -231,17 +270,11 @@ def attention_layer_extra(args, env):
         ops.bsattn_fwd_strided(plan, qh, kh, v_view, scale, out=att_view)
         torch.mm(att, w_out.t(), out=y)
 
-    res = {}
-    for name, f in (("fused_qkv", fused_path), ("hipblaslt_qkv", unfused_path)):
-        reps = max(10, args.steps)
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(reps + 2)]
-        for a, b in ev:
-            a.record()
-            f()
-            b.record()
-        torch.cuda.synchronize()
-        res[name + "_ms"] = round(float(np.mean([a.elapsed_time(b) for a, b in ev[2:]])), 4)
+    med = interleaved_medians({"fused_qkv": fused_path, "hipblaslt_qkv": unfused_path},
+                              reps=max(12, args.steps))
+    res = {"timing": "medians of interleaved calls"}
+    for name, ms in med.items():
+        res[name + "_ms"] = round(ms, 4)
     flops = (2.0 * S * C_HIDDEN * 3 * inner + plan.nnz * H * FLOP_PER_TILE_HEAD
              + 2.0 * S * inner * C_HIDDEN)
     res["layer_tflop"] = round(flops / 1e12, 4)
@@ -399,23 +432,41 @@ def main() -> int:
         k_in = (hidden @ ((torch.randn((5120, inner), generator=g, device=dev) * 0.02)
                           .to(torch.bfloat16)))[:S]
         del hidden, wq
-        reps = max(10, args.steps)
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(reps + 3)]
-        for i, (a, b) in enumerate(evs):
-            a.record()
-            ops.qk_norm_rope(q_in, k_in, gq, gk, pos, ax, inv, heads=H, eps=C.QK_EPS,
-                             seq_pad=S_pad, out=(qh, kh, None))
-            b.record()
-        torch.cuda.synchronize()
-        p5 = float(np.mean([a.elapsed_time(b) for a, b in evs[3:]]))
+        # The same bytes moved by a plain device copy and by the pure token ->
+        # head-major relayout of Q and K (h3hip_head_major, no arithmetic): the
+        # ceilings the prologue's layout change runs against, in the same run.
+        qk_in = torch.empty((S, 2 * inner), dtype=torch.bfloat16, device=dev)
+        qk_in[:, :inner].copy_(q_in)
+        qk_in[:, inner:].copy_(k_in)
+        qk_hm = torch.empty((2 * H, S_pad, D), dtype=torch.bfloat16, device=dev)
+        copy_src = torch.empty(2 * S_pad * inner, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        copy_dst = torch.empty_like(copy_src)
+        med = interleaved_medians({
+            "prologue": lambda: ops.qk_norm_rope(q_in, k_in, gq, gk, pos, ax, inv, heads=H,
+                                                 eps=C.QK_EPS, seq_pad=S_pad,
+                                                 out=(qh, kh, None)),
+            "relayout": lambda: ops.head_major(qk_in, heads=2 * H, seq_pad=S_pad, out=qk_hm),
+            "copy": lambda: copy_dst.copy_(copy_src),
+        }, reps=max(12, args.steps))
         b5 = 2 * S * inner * 2 + 2 * S_pad * inner * 2 + S * 12 + 2 * D * 2
+        b_rel = 2 * S * inner * 2 + 2 * S_pad * inner * 2
+        b_copy = 2 * copy_src.numel() * 2
+        gbps = lambda b, ms: round(b / (ms * 1e-3) / 1e9, 1)
+        p5 = med["prologue"]
         extras["cfg5_prologue_qk"] = {
-            "ms": round(p5, 4), "bytes": b5, "gbps": round(b5 / (p5 * 1e-3) / 1e9, 1),
+            "timing": "medians of interleaved calls",
+            "ms": round(p5, 4), "bytes": b5, "gbps": gbps(b5, p5),
             "hbm_peak_frac": round(b5 / (p5 * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            "relayout_ceiling_ms": round(med["relayout"], 4),
+            "relayout_ceiling_gbps": gbps(b_rel, med["relayout"]),
+            "copy_ceiling_ms": round(med["copy"], 4),
+            "copy_ceiling_gbps": gbps(b_copy, med["copy"]),
+            "frac_of_relayout_ceiling": round(gbps(b5, p5) / gbps(b_rel, med["relayout"]), 4),
             "traffic": read_traffic("qk_norm_rope_cfg5_traffic.txt"),
         }
-        del q_in, k_in
+        result["prologue_relayout_ceiling_gbps"] = extras["cfg5_prologue_qk"]["relayout_ceiling_gbps"]
+        result["prologue_copy_ceiling_gbps"] = extras["cfg5_prologue_qk"]["copy_ceiling_gbps"]
+        del q_in, k_in, qk_in, qk_hm, copy_src, copy_dst
         extras["cfg3_qkv_proj"] = qkv_projection_extra(args, env=locals())
         extras["cfg3_attention_layer"] = attention_layer_extra(args, env=locals())
         for name in ("cfg3_1344x768x5s_frame0", "cfg2_864x480x7s", "cfg4_dense_864x480x7s",
@@ -425,16 +476,12 @@ def main() -> int:
             qq = torch.randn((sh.heads, p.seq_pad, D), generator=g, device=dev).to(torch.bfloat16)
             kk = torch.randn_like(qq)
             vv = torch.randn_like(qq)
-            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for _ in range(8)]
-            for a, b in evs:
-                a.record()
-                ops.bsattn_fwd(p, qq, kk, vv, scale)
-                b.record()
-            torch.cuda.synchronize()
-            ms = float(np.mean([a.elapsed_time(b) for a, b in evs[2:]]))
+            oo = torch.empty_like(qq)
+            ms = interleaved_medians({"attn": lambda: ops.bsattn_fwd(p, qq, kk, vv, scale, out=oo)},
+                                     reps=max(12, args.steps))["attn"]
             fl = p.nnz * sh.heads * FLOP_PER_TILE_HEAD
-            extras[name] = {"attn_ms": round(ms, 4), "active_tiles_per_head": p.nnz,
+            extras[name] = {"timing": "median of 12+ calls", "attn_ms": round(ms, 4),
+                            "active_tiles_per_head": p.nnz,
                             "density": round(p.density, 5),
                             "tflops_active": round(fl / (ms * 1e-3) / 1e12, 3),
                             "mfma_peak_frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
@@ -443,7 +490,7 @@ def main() -> int:
                 extras[name]["heads"] = sh.heads
                 extras[name]["token_density"] = round(h3hip.axial_token_density(
                     sh.prefix_len, sh.frames, sh.height, sh.width, kw["landmarks"]), 5)
-            del qq, kk, vv
+            del qq, kk, vv, oo
             p.close()
         result["extras"] = extras
 

@@ -187,6 +187,16 @@ int h3hip_qk_norm_rope(const void* q_in, const void* k_in, int64_t ld_in, const 
                        int32_t rounding, int32_t seq_len, int32_t seq_pad, int32_t heads,
                        int32_t head_dim, void* q_out, void* k_out, void* v_out, void* stream);
 
+/* Token-major -> head-major copy: the [S, heads, head_dim] -> [heads, S, head_dim]
+ * transposes of AttentionLayer.sdpa (Sources/H3Modules/DiTBlock.swift:297-300)
+ * materialised. in: device bf16 [seq_len, >= heads*head_dim], row stride ld_in
+ * elements (V of a fused Q|K|V projection: in = qkv + 2*heads*head_dim,
+ * ld_in = 3*heads*head_dim). out: device bf16 [heads, seq_pad, head_dim]; rows
+ * >= seq_len are zeroed. No arithmetic: every row is moved unchanged.
+ * Declines unless head_dim == 128. */
+int h3hip_head_major(const void* in, int64_t ld_in, int32_t seq_len, int32_t seq_pad,
+                     int32_t heads, int32_t head_dim, void* out, void* stream);
+
 /* The rotation table of a render: H3RoPE.rotationTable(H3RoPE.angles(pos,
  * inv_freq)) (Sources/H3Modules/H3Transformer.swift:62-78), which
  * prepareRender builds once per render (:271-273) and every layer's

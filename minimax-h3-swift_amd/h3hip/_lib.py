@@ -99,6 +99,8 @@ SIGNATURES = {
                                           ctypes.c_float, _vp, _vp, _vp, ctypes.c_int32,
                                           ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                           ctypes.c_int32, ctypes.c_int32, _vp, _vp, _vp, _vp]),
+    "h3hip_head_major": (ctypes.c_int, [_vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                                        ctypes.c_int32, ctypes.c_int32, _vp, _vp]),
     "h3hip_rope_table": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32,
                                         ctypes.c_int32, _vp, _vp]),
     "h3hip_qkv_proj": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int32,

@@ -50,6 +50,22 @@ def dense_fp32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, seq_len: int, 
     return out
 
 
+def span_error(plan: TilePlan, q, k, v, prefix_len: int, want=None) -> dict:
+    """Relative RMS of the block-sparse output over ``plan``'s tiles against
+    dense fp32 attention, over all rows, the prefix rows and the video rows
+    (the spans of AxialMeasureTests.swift:83-96) -- for any tile plan, e.g. the
+    local-window rules of the benchmark shapes."""
+    seq_len = plan.seq_len
+    scale = 1.0 / math.sqrt(q.shape[2])
+    if want is None:
+        want = dense_fp32(q, k, v, seq_len, scale)
+    got = ops.bsattn_fwd(plan, q, k, v, scale)[:, :seq_len]
+    torch.cuda.synchronize()
+    return dict(tile_density=plan.density, total=rel_rms(got, want),
+                prefix=rel_rms(got[:, :prefix_len], want[:, :prefix_len]) if prefix_len else 0.0,
+                video=rel_rms(got[:, prefix_len:], want[:, prefix_len:]))
+
+
 def per_span_error(q, k, v, seq_len: int, prefix_len: int, frames: int, height: int, width: int,
                    landmark_counts=(2, 3, 5, 9), want=None):
     """Rows of (landmarks, token density, tile density, total, prefix, video)

@@ -133,6 +133,29 @@ def qk_norm_rope(q_in: torch.Tensor, k_in: torch.Tensor, q_gamma: torch.Tensor,
     return q_out, k_out, v_out
 
 
+def head_major(x: torch.Tensor, *, heads: int, head_dim: int = 128, seq_pad: int | None = None,
+               out: torch.Tensor | None = None):
+    """Token-major [S, >= heads*head_dim] bf16 (row stride free, unit column
+    stride) -> head-major [heads, seq_pad, head_dim], rows >= S zero: the
+    materialised transpose of AttentionLayer.sdpa. Returns None when declined."""
+    if x.dim() != 2 or x.stride(1) != 1 or x.shape[1] < heads * head_dim:
+        raise ValueError(f"x must be a 2-D view [S, >= {heads * head_dim}] with unit column "
+                         f"stride, got shape {tuple(x.shape)} strides {x.stride()}")
+    S = x.shape[0]
+    seq_pad = seq_pad or ((S + L.TILE - 1) // L.TILE) * L.TILE
+    shape = (heads, seq_pad, head_dim)
+    if out is not None:
+        _require_out(out, shape, x.device)
+    _require_gpu_bf16("x", x)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.bfloat16, device=x.device)
+    rc = L.lib().h3hip_head_major(_ptr(x), x.stride(0), S, seq_pad, heads, head_dim, _ptr(out),
+                                  _stream(x))
+    if L.check(rc, allow_declined=True) == L.DECLINED:
+        return None
+    return out
+
+
 def rope_table(pos: torch.Tensor, pair_axis: torch.Tensor, pair_inv: torch.Tensor, *,
                rot: int | None = None, rounding: int = L.ROUND_REFERENCE,
                out: torch.Tensor | None = None) -> torch.Tensor:

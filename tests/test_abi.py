@@ -123,6 +123,11 @@ def test_projection_and_rope_table_refusals(h3):
         rc = lib.h3hip_qkv_proj(buf, 128, buf, 128, hidden, None, None, 1e-6, None, 128, 0, 4,
                                 128, 2, 128, buf, buf, buf, None)
         assert rc == _lib.EINVAL and "hidden" in h3.last_error(), hidden
+    # h3hip_head_major: head_dim 64 declines, NULL and a short row stride are refused.
+    assert lib.h3hip_head_major(buf, 256, 4, 128, 4, 64, buf, None) == D
+    assert lib.h3hip_head_major(None, 512, 4, 128, 4, 128, buf, None) == _lib.EINVAL
+    rc = lib.h3hip_head_major(buf, 256, 4, 128, 4, 128, buf, None)
+    assert rc == _lib.EINVAL and "ld_in" in h3.last_error()
     assert lib.h3hip_rope_table(None, None, None, 128, 0, 4, None, None) == _lib.EINVAL
     rc = lib.h3hip_rope_table(buf, buf, buf, 127, 0, 4, buf, None)
     assert rc == _lib.EINVAL and "rot" in h3.last_error()

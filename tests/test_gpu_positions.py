@@ -79,9 +79,9 @@ def test_prologue_on_packed_positions(h3, orc, rounding):
                                torch.from_numpy(axis).cuda(), torch.from_numpy(inv).cuda(),
                                heads=H, eps=H3_EPS, rot=H3_ROT, rounding=rounding)
     torch.cuda.synchronize()
-    for name, got, x_bits, gam in (("q", q, qkv, qg),
-                                   ("k", k, np.ascontiguousarray(qkv[:, inner:]), kg)):
-        want = orc.qk_norm_rope(x_bits, 3 * inner, S, S_pad, H, D, gam, H3_EPS, pos, axis, inv,
+    for name, got, x_bits, gam in (("q", q, np.ascontiguousarray(qkv[:, :inner]), qg),
+                                   ("k", k, np.ascontiguousarray(qkv[:, inner:2 * inner]), kg)):
+        want = orc.qk_norm_rope(x_bits, inner, S, S_pad, H, D, gam, H3_EPS, pos, axis, inv,
                                 H3_ROT, rounding)
         rel, ulp, same = gate(bits(got), want)
         print(f"{name} rounding {rounding}: rel RMS {rel:.2e}, worst ulp {ulp:.2f}, "
@@ -109,8 +109,9 @@ def test_rope_table_on_packed_positions(h3, orc):
     ulp = np.abs(gf.view(np.int32).astype(np.int64) - want32.view(np.int32).astype(np.int64))
     print(f"packed table: bf16 identical {same:.6f} (max {d16.max()} ulp), fp32 max {ulp.max()} ulp")
     assert same >= 0.999 and d16.max() <= 1 and ulp.max() <= 2
-    # Against the closed form in double for the largest angles.
-    ang = pos[:, axis].astype(np.float64) * inv.astype(np.float64)
+    # Against the closed form in double for the largest angles: cos and sin of
+    # the fp32 angle fp32(pos * inv_freq) that H3RoPE.angles forms.
+    ang = (pos[:, axis] * inv[None, :]).astype(np.float32).astype(np.float64)
     big = ang > 50
     assert big.any()
     assert np.allclose(gf[..., 0][big], np.cos(ang[big]), atol=2e-6)
