@@ -156,6 +156,19 @@ int h3hip_schedule(const int32_t* row_ptr, int32_t n_tiles, int32_t heads, int32
  * (Sources/H3Attention/AxialReference.swift:42-84), reduced onto tiles. */
 int h3hip_mask_from_rule(const h3hip_mask_rule* rule, uint8_t* d_bitmap, void* stream);
 
+/* h3hip_mask_from_rule without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The rule's flag tables (BAND global columns, landmark frames) and the host
+ * lists they come from are staged in a static per-GPU scratch array of
+ * 192 KiB inside the library, instead of a temporary allocation: at most
+ * 32,768 flags (tile columns or frames) and 32,768 listed entries, larger
+ * rules are refused with H3HIP_EINVAL. Same bitmap as h3hip_mask_from_rule.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap on one
+ * GPU (concurrent streams or threads) race. Synchronises `stream` when it
+ * staged a host list. */
+int h3hip_mask_from_rule_noalloc(const h3hip_mask_rule* rule, uint8_t* d_bitmap, void* stream);
+
 /* Block mask -> CSR on the device. d_bitmap [nq * nk] bytes; d_row_ptr[nq + 1]
  * and d_col_idx[col_capacity] are written. Synchronises `stream` once to read
  * nnz; returns H3HIP_EINVAL (with *nnz set) if col_capacity < nnz. Ascending

@@ -247,6 +247,50 @@ static int launch_mask(const h3hip_mask_rule* r, uint8_t* d_bitmap, hipStream_t 
   return check_launch("mask_rule_kernel");
 }
 
+// ---------------------------------------------- static scratch (no allocation)
+
+// Device scratch for h3hip_mask_from_rule_noalloc: the rule's flag tables
+// (BAND global columns, landmark frames) and the host lists they are built
+// from, in one file-scope array per GPU that lives until the process ends.
+// Layout: column flags [0, 32 KiB), frame flags [32 KiB, 64 KiB), the staged
+// int32 list [64 KiB, 192 KiB).
+constexpr int32_t kScratchFlags = 32768;   // max tile columns / frames
+constexpr int32_t kScratchList = 32768;    // max global columns / landmarks
+constexpr size_t kScratchBytes = 2 * kScratchFlags + 4 * (size_t)kScratchList;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// The scratch array's device address on each GPU, looked up once per device.
+constexpr int kMaxDevices = 64;
+static uint8_t* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+static int scratch_on_current_device(uint8_t** out) {
+  int dev = 0;
+  H3_HIP_CHECK(hipGetDevice(&dev));
+  H3_REQUIRE(dev >= 0 && dev < kMaxDevices, H3HIP_EDEVICE, "device %d beyond %d", dev,
+             kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    H3_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    H3_REQUIRE(p != nullptr, H3HIP_EHIP, "hipGetSymbolAddress returned NULL for the scratch");
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return H3HIP_OK;
+}
+
+// flags[0 .. n_flags) = 0, then flags[list[i]] = 1 for i < n_list (list
+// entries are validated on the host). One workgroup; a fill kernel rather
+// than a memset so the clear is an ordinary kernel node.
+__global__ __launch_bounds__(256) void flags_from_list_kernel(uint8_t* flags, int32_t n_flags,
+                                                              const int32_t* list,
+                                                              int32_t n_list) {
+  for (int32_t i = threadIdx.x; i < n_flags; i += 256) flags[i] = 0;
+  __syncthreads();
+  for (int32_t i = threadIdx.x; i < n_list; i += 256) flags[list[i]] = 1;
+}
+
 static int csr_on_device(const uint8_t* d_bitmap, int32_t nq, int32_t nk, int32_t* d_row_ptr,
                          hipStream_t stream, int64_t* nnz) {
   row_count_kernel<<<nq, 256, 0, stream>>>(d_bitmap, nk, d_row_ptr);
@@ -289,6 +333,58 @@ int h3hip_mask_from_rule(const h3hip_mask_rule* rule, uint8_t* d_bitmap, void* s
   if (rc) return rc;
   // The scratch arrays are freed on return; make sure the kernel is done with them.
   if (scratch.d) H3_HIP_CHECK(hipStreamSynchronize(as_stream(stream)));
+  return H3HIP_OK;
+}
+
+int h3hip_mask_from_rule_noalloc(const h3hip_mask_rule* rule, uint8_t* d_bitmap, void* stream) {
+  int rc = validate_rule(rule);
+  if (rc) return rc;
+  H3_REQUIRE(d_bitmap != nullptr, H3HIP_EINVAL, "d_bitmap is NULL");
+  hipStream_t st = as_stream(stream);
+  const int32_t n_tiles = (rule->seq_len + H3HIP_TILE - 1) / H3HIP_TILE;
+  if (rule->kind == H3HIP_RULE_BITMAP) {
+    H3_HIP_CHECK(hipMemcpyAsync(d_bitmap, rule->bitmap, (size_t)n_tiles * n_tiles,
+                                hipMemcpyHostToDevice, st));
+    return H3HIP_OK;
+  }
+  const bool band = rule->kind == H3HIP_RULE_BAND;
+  const bool lattice = rule->kind == H3HIP_RULE_LOCAL || rule->kind == H3HIP_RULE_AXIAL;
+  const int32_t n_list = band ? rule->n_global_cols : lattice ? rule->n_landmarks : 0;
+  const int32_t n_flags = band ? n_tiles : lattice ? rule->frames : 0;
+  const bool uses_scratch = n_list > 0 || band;
+  H3_REQUIRE(!uses_scratch || n_flags <= kScratchFlags, H3HIP_EINVAL,
+             "%d %s exceed the static scratch's %d flags", n_flags,
+             band ? "tile columns" : "frames", kScratchFlags);
+  H3_REQUIRE(n_list <= kScratchList, H3HIP_EINVAL,
+             "%d listed %s exceed the static scratch's %d entries", n_list,
+             band ? "global columns" : "landmarks", kScratchList);
+  RuleDev dev{rule->kind, rule->seq_len, rule->prefix_len, rule->frames, rule->height,
+              rule->width, rule->frame_window, rule->spatial_tile_h, rule->spatial_tile_w,
+              rule->spatial_window, rule->band, n_tiles, nullptr, nullptr};
+  bool staged = false;
+  if (uses_scratch) {
+    uint8_t* sp = nullptr;
+    rc = scratch_on_current_device(&sp);
+    if (rc) return rc;
+    uint8_t* flags = band ? sp : sp + kScratchFlags;
+    int32_t* list = reinterpret_cast<int32_t*>(sp + 2 * kScratchFlags);
+    if (n_list > 0) {
+      H3_HIP_CHECK(hipMemcpyAsync(list, band ? rule->global_cols : rule->landmark_frames,
+                                  sizeof(int32_t) * n_list, hipMemcpyHostToDevice, st));
+      staged = true;
+    }
+    flags_from_list_kernel<<<1, 256, 0, st>>>(flags, n_flags, list, n_list);
+    rc = check_launch("flags_from_list_kernel");
+    if (rc) return rc;
+    if (band) dev.col_global = flags;
+    else dev.frame_landmark = flags;
+  }
+  mask_rule_kernel<<<dim3(n_tiles, n_tiles), 256, 0, st>>>(dev, d_bitmap);
+  rc = check_launch("mask_rule_kernel");
+  if (rc) return rc;
+  // The rule's host lists were staged asynchronously: keep them alive until the
+  // copy has consumed them.
+  if (staged) H3_HIP_CHECK(hipStreamSynchronize(st));
   return H3HIP_OK;
 }
 

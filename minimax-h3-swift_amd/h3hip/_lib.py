@@ -92,6 +92,7 @@ SIGNATURES = {
     "h3hip_schedule": (ctypes.c_int, [_i32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                       _i32p, _i32p]),
     "h3hip_mask_from_rule": (ctypes.c_int, [ctypes.POINTER(MaskRuleC), _vp, _vp]),
+    "h3hip_mask_from_rule_noalloc": (ctypes.c_int, [ctypes.POINTER(MaskRuleC), _vp, _vp]),
     "h3hip_tiles_from_mask": (ctypes.c_int, [_vp, ctypes.c_int32, ctypes.c_int32, _vp, _vp,
                                              ctypes.c_int64, ctypes.POINTER(ctypes.c_int64),
                                              _vp]),
