@@ -69,63 +69,6 @@ __device__ __forceinline__ void store16(uint16_t* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
-__device__ __forceinline__ void unpack8(u32x4 w, float* f) {
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    f[2 * i] = bf16_lo(w[i]);
-    f[2 * i + 1] = bf16_hi(w[i]);
-  }
-}
-
-__device__ __forceinline__ u32x4 pack8(const float* f) {
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; i++) r[i] = cvt_pk(f[2 * i], f[2 * i + 1]);
-  return r;
-}
-
-// DPP controls used by the 8-lane reduction.
-constexpr int kDppHalfMirror = 0x141;   // lane j <- lane 7 - j within 8 lanes
-constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
-constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
-
-template <int kCtrl>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
-}
-
-// Mean of squares of the row (fixed fp32 order, see the file header) and the
-// normalised values y = (x * r) * g.
-__device__ __forceinline__ void rms_normalise(const float* x, const float* g, float eps,
-                                              float* y) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; i++) s = fmaf(x[i], x[i], s);
-  s = s + dpp<kDppHalfMirror>(s);
-  s = s + dpp<kDppQuadXor2>(s);
-  s = s + dpp<kDppQuadXor1>(s);
-  const float ms = s * (1.0f / kHeadDim);
-  const float r = rsqrt_rounded(ms + eps);
-#pragma unroll
-  for (int i = 0; i < 16; i++) y[i] = (x[i] * r) * g[i];
-}
-
-// One row slice: x holds chunk a (x[0..7]) and chunk b (x[8..15]). kFull:
-// every lane is a pair lane (rot == 128).
-template <int kMode, bool kFull>
-__device__ __forceinline__ void norm_rope(const float* x, const float* g, bool pair_lane,
-                                          const RopeEntry* tab, float eps, u32x4& out_a,
-                                          u32x4& out_b) {
-  float y[16];
-  rms_normalise(x, g, eps, y);
-  const bool rotate = kFull || pair_lane;
-  float oa[8], ob[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) rope_pair<kMode>(y[i], y[8 + i], tab[i], rotate, oa[i], ob[i]);
-  out_a = pack8(oa);
-  out_b = pack8(ob);
-}
-
 // Workgroup: kTok tokens x all heads. Row groups of 8 lanes; the first half of
 // the groups normalise Q rows, the second half K rows, each streaming its rows
 // with the next row's loads issued before the current row is computed. V rows

@@ -6,32 +6,35 @@
 // [heads, seq_pad, 128], the layout the attention reads, without the token-major
 // qkv ever being written and read back.
 //
-// GEMM: C^T[n, m] = sum_k W[n, k] x[m, k] with v_mfma_f32_32x32x16_bf16, the W
-// rows as the A operand and the x rows as B. Each accumulator lane therefore
-// holds one token and 16 output channels: a token's 128 channels of one head
-// sit in one lane pair (lanes l and l ^ 32), so the row norm needs one exchange
-// between the half-waves and every RoPE pair (p, p + rot/2) is in one lane.
+// GEMM: C^T[n, m] = sum_k W[n, k] x[m, k] with v_mfma_f32_16x16x32_bf16, the W
+// rows as the A operand and the x rows as B. At random bf16 operands the chip
+// runs this GEMM at its power limit, and the 16 x 16 x 32 form does about 11%
+// more FLOPs per joule than the 32 x 32 x 16 form (sustained-MFMA measurement
+// on MI355X: 2.00 against 1.80 PFLOP/s; equal at zero operands).
 //
 // Workgroup: 256 tokens x 256 output channels (two heads of one of Q, K, V),
 // 8 waves, two per SIMD. Wave w owns head (w >> 2) of the tile and tokens
-// 64 (w & 3) .. +63: 4 x 2 accumulators of 32 x 32. The reduction runs in steps
+// 64 (w & 3) .. +63: 8 x 4 accumulators of 16 x 16. The reduction runs in steps
 // of 64: the W and x tiles of a step (256 rows of 128 bytes each, 16-byte
 // chunks XOR-swizzled so operand reads are conflict-free) are double-buffered
-// in LDS and filled by HBM -> LDS buffer loads two steps ahead. One barrier per
-// step, placed before the step's last sub-step, whose operands are already in
-// registers; the loads of step t + 2 follow it, issued by one wave per SIMD
-// (16 x 1 KiB each), so the other wave of the SIMD never waits on a load issue.
-// The instruction order inside a sub-step is pinned with sched_barrier.
+// in LDS and filled by HBM -> LDS buffer loads two steps ahead. A step is two
+// 32-deep sub-steps of 32 MFMAs; the operands of the next sub-step are read
+// while the current one multiplies (x operands double-buffered, each W operand
+// re-read into its register right after its last MFMA). One barrier per step,
+// before the second sub-step, whose operands are then in registers; the loads
+// of step t + 2 follow it, issued by one wave per SIMD (16 x 1 KiB each), so
+// the other wave of the SIMD never waits on a load issue. The instruction
+// order is pinned with sched_barrier.
 //
-// Epilogue (Q and K): the fp32 accumulators are rounded to bf16 (the bf16
-// matmul output the reference normalises), the mean of squares is summed in
-// exactly the order the prologue kernel uses (the two half-waves each run half
-// of the fixed-order chains, exchanged with permlane32_swap), the rotation
-// takes its (c, s) from the render's rotation table -- the reference's
-// ropeTable, built once per render by h3hip_rope_table with the prologue's own
-// entry function -- and norm and rotation use the prologue's arithmetic
-// (norm_rope.h). The output equals h3hip_qk_norm_rope applied to this kernel's
-// bf16 GEMM result, bit for bit.
+// Epilogue: the fp32 accumulators are rounded to bf16 (the bf16 matmul output
+// the reference normalises) and written as token rows to the wave's own 8 KiB
+// of LDS. Each row is then read back in the prologue kernel's 8-lane row layout
+// and, for Q and K, normalised and rotated by the same device code the
+// prologue runs (norm_rope.h), with (c, s) from the render's rotation table --
+// the reference's ropeTable, built once per render by h3hip_rope_table with
+// the prologue's own entry function. The output therefore equals
+// h3hip_qk_norm_rope applied to this kernel's bf16 GEMM result, bit for bit.
+// Rows are stored whole: 8 consecutive head-major rows (2 KiB) per pass.
 #include <type_traits>
 
 #include "common.h"
@@ -60,25 +63,37 @@ constexpr int kHD = 128;                  // head_dim
 constexpr int kPWaves = 8;                // per workgroup: 2 per head x kPWaves/2 token slices
 constexpr int kPThreads = 64 * kPWaves;
 constexpr int kTokWave = 2 * kPM / kPWaves;   // tokens per wave
-constexpr int kMB = kTokWave / 32;            // 32-token accumulator blocks per wave
+constexpr int kMB = kTokWave / 16;            // 16-token accumulator blocks per wave
+constexpr int kNB = kHD / 16;                 // 16-channel accumulator blocks per wave
 constexpr int kRowsWave = kPM / kPWaves;      // rows of each operand tile a wave loads
 constexpr int kLoadsTile = kRowsWave / 8;     // 1 KiB loads per operand tile per wave
+constexpr int kLoadsStep = 4 * kLoadsTile;    // loads per step of a loading wave
 constexpr int kGroupM = 4;                // token tiles per launch-order group
 constexpr int kXcds = 8;
 constexpr int kTileElems = kPM * kPK;     // one operand tile (W or x) of a step
 constexpr int kStageElems = 2 * kTileElems;
+constexpr int kMfmaSub = kNB * kMB;       // MFMAs per 32-deep sub-step
 // s_waitcnt immediate for vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9).
 constexpr int kPWaitVmcnt0 = 0x0F70;
 // vmcnt(n), lgkmcnt and expcnt unconstrained (vmcnt bits 3:0 and 15:14).
 constexpr int wait_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 constexpr int kPWaitAll = 0x0070;         // vmcnt(0) lgkmcnt(0)
 constexpr int kPBufferWord3 = 0x00020000;
+static_assert(kMfmaSub == 2 * kLoadsStep, "one load per two MFMAs of the second sub-step");
 
 typedef int i32x4p __attribute__((ext_vector_type(4)));
 
-// 16-byte chunk c of the 128-byte row r sits at c ^ ((r >> 1) & 7): the 16
-// rows of a 16-lane read phase cover both row parities x 8 chunk positions.
+// 16-byte chunk c of the 128-byte operand row r sits at c ^ ((r >> 1) & 7):
+// the 16 rows of a 16-lane read phase cover both row parities x 8 chunk
+// positions. Rows 16 apart share the swizzle.
 __device__ __forceinline__ int p_swz(int r) { return (r >> 1) & 7; }
+
+// 16-byte chunk c of the 256-byte epilogue row r sits at c ^ e_swz(r): the
+// 16 rows one accumulator write covers hit 16 distinct positions (every 8-byte
+// slot of a bank window once per 32 lanes), and rows r, r ^ 1 map the chunks
+// 0..7 onto complementary halves, so the 2 rows x 8 lanes of a 16-lane read
+// phase are conflict-free.
+__device__ __forceinline__ int e_swz(int r) { return ((r & 1) << 3) | ((r >> 1) & 7); }
 
 __device__ __forceinline__ i32x4p proj_rsrc(const void* base, uint32_t bytes) {
   const uint64_t b = reinterpret_cast<uint64_t>(base);
@@ -114,7 +129,10 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nh = wave / (kPWaves / 2), mq = wave % (kPWaves / 2);
-  const int li = lane & 31, hh = lane >> 5;
+  // v_mfma_f32_16x16x32_bf16 layout: lane (g = lane/16, lr = lane%16) holds
+  // row lr of an A block and column lr of a B block at k = 8g .. 8g + 7, and
+  // rows 4g .. 4g + 3 of column lr of the 16 x 16 result.
+  const int lr = lane & 15, g = lane >> 4;
   // Tile order. Workgroup b runs on XCD b % 8 (round-robin dispatch) and
   // XCD x takes the tiles [x q + min(x, r), ...) of a grouped order (total =
   // 8 q + r), so the workgroups one XCD runs at once cover a compact block
@@ -134,15 +152,18 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   const int part = n0 / inner;                        // uniform over the tile
   const int head = (n0 - part * inner) / kHD + nh;    // this wave's head
 
-  // Operand offsets within a tile (elements): A = W row nh*128 + 32nb + li,
-  // B = x row 64mq + 32mb + li; chunk 2s + hh of the step's 64 columns.
-  int a_row[4], b_row[kMB];
+  // Operand offsets within a stage (elements). A block nb = W row
+  // nh*128 + 16nb + lr, B block mb = x row 64mq + 16mb + lr; sub-step u reads
+  // chunk 4u + g of the step's 8. The block index is an immediate offset.
+  const int a_row0 = nh * kHD + lr, b_row0 = kTokWave * mq + lr;
+  int a_off[2], b_off[2];
 #pragma unroll
-  for (int nb = 0; nb < 4; nb++) a_row[nb] = nh * 128 + 32 * nb + li;
-#pragma unroll
-  for (int mb = 0; mb < kMB; mb++) b_row[mb] = kTokWave * mq + 32 * mb + li;
-  auto operand = [&](const uint16_t* tile, int row, int s) __attribute__((always_inline)) {
-    return *reinterpret_cast<const bf16x8*>(tile + row * kPK + (((2 * s + hh) ^ p_swz(row)) * 8));
+  for (int u = 0; u < 2; u++) {
+    a_off[u] = a_row0 * kPK + (((4 * u + g) ^ p_swz(a_row0)) * 8);
+    b_off[u] = kTileElems + b_row0 * kPK + (((4 * u + g) ^ p_swz(b_row0)) * 8);
+  }
+  auto operand = [&](const uint16_t* stage, int off, int blk) __attribute__((always_inline)) {
+    return *reinterpret_cast<const bf16x8*>(stage + off + blk * 16 * kPK);
   };
 
   // HBM -> LDS: wave w moves rows 32w .. 32w+31 of the W tile and of the x
@@ -152,30 +173,38 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   const i32x4p x_rsrc = proj_rsrc(a.x, (uint32_t)((a.seq_len - 1) * a.ldx + a.hidden) * 2u);
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(proj_lds_address(lds));
   const int lw = wave & 3;   // loading wave: rows of waves lw and lw + 4
-  int w_voff[2 * kLoadsTile], x_voff[2 * kLoadsTile];
+  // Load ii of a tile covers row r(ii) = 32 lw + 128 (ii >> 2) + 8 (ii & 3) +
+  // lane / 8; rows 16 apart share the chunk swizzle, so the source chunk
+  // depends on ii only through ii & 1. x offsets stay whole in the lane offset,
+  // which the hardware range-checks (rows >= seq_len read as 0); every W row
+  // of the tile exists, so W's row step goes into the scalar offset and two
+  // lane offsets serve its eight loads.
+  int w_voff[2], x_voff[2 * kLoadsTile];
 #pragma unroll
   for (int i = 0; i < 2 * kLoadsTile; i++) {
     const int r = kRowsWave * (lw + 4 * (i >> 2)) + (lane >> 3) + 8 * (i & 3);
     const int src_chunk = (lane & 7) ^ p_swz(r);
-    w_voff[i] = (n0 + r) * (int)a.ldw * 2 + src_chunk * 16;
-    x_voff[i] = (m0 + r) * (int)a.ldx * 2 + src_chunk * 16;   // rows >= seq_len: out of range, read as 0
+    if (i < 2) w_voff[i] = (n0 + r) * (int)a.ldw * 2 + src_chunk * 16;
+    x_voff[i] = (m0 + r) * (int)a.ldx * 2 + src_chunk * 16;
   }
-  // Load i of step t (i < kLoadsTile: W rows, then x rows) into stage st.
+  // Load i of step t (i < 2 kLoadsTile: W rows, then x rows) into stage st.
   auto dma = [&](int t, int st, int i) __attribute__((always_inline)) {
     const bool is_x = i >= 2 * kLoadsTile;
     const int ii = is_x ? i - 2 * kLoadsTile : i;
     const uint32_t dst = lds_base + 2 * (st * kStageElems + (is_x ? kTileElems : 0) +
                                          (kRowsWave * (lw + 4 * (ii >> 2)) + 8 * (ii & 3)) * kPK);
-    proj_dma16(is_x ? x_rsrc : w_rsrc, dst, is_x ? x_voff[ii] : w_voff[ii], t * kPK * 2);
+    if (is_x)
+      proj_dma16(x_rsrc, dst, x_voff[ii], t * kPK * 2);
+    else
+      proj_dma16(w_rsrc, dst, w_voff[ii & 1],
+                 t * kPK * 2 + (8 * (ii & 2) + 4 * kRowsWave * (ii >> 2)) * (int)a.ldw * 2);
   };
 
-  f32x16 acc[4][kMB];
+  f32x4 acc[kNB][kMB];
 #pragma unroll
-  for (int nb = 0; nb < 4; nb++)
+  for (int nb = 0; nb < kNB; nb++)
 #pragma unroll
-    for (int mb = 0; mb < kMB; mb++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[nb][mb][r] = 0.f;
+    for (int mb = 0; mb < kMB; mb++) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Stage st of the LDS ring holds step t with st = t & 1. Steps 0 and 1 are
   // loaded up front; the loads of step t + 2 are issued right after the
@@ -184,220 +213,154 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   const int steps = a.hidden / kPK;
   if (wave < 4) {
 #pragma unroll
-    for (int i = 0; i < 4 * kLoadsTile; i++) dma(0, 0, i);
+    for (int i = 0; i < kLoadsStep; i++) dma(0, 0, i);
     if (steps > 1) {
 #pragma unroll
-      for (int i = 0; i < 4 * kLoadsTile; i++) dma(1, 1, i);
-      __builtin_amdgcn_s_waitcnt(wait_vmcnt(4 * kLoadsTile));
+      for (int i = 0; i < kLoadsStep; i++) dma(1, 1, i);
+      __builtin_amdgcn_s_waitcnt(wait_vmcnt(kLoadsStep));
     } else {
       __builtin_amdgcn_s_waitcnt(kPWaitVmcnt0);
     }
   }
   __syncthreads();
 
-  bf16x8 A[2][4], B[2][kMB];
-  auto read_ops = [&](int buf, const uint16_t* stage, int sub) __attribute__((always_inline)) {
+  // A: the W operands of the current sub-step, each replaced by the next
+  // sub-step's right after its last MFMA. B: the x operands, double-buffered
+  // (buffer u for sub-step u).
+  bf16x8 A[kNB], B[2][kMB];
 #pragma unroll
-    for (int nb = 0; nb < 4; nb++) A[buf][nb] = operand(stage, a_row[nb], sub);
+  for (int nb = 0; nb < kNB; nb++) A[nb] = operand(lds, a_off[0], nb);
 #pragma unroll
-    for (int mb = 0; mb < kMB; mb++) B[buf][mb] = operand(stage + kTileElems, b_row[mb], sub);
-  };
-  // Operand i of sub-step sub (i < 4: A block i, else B block i - 4).
-  auto read_op = [&](int buf, const uint16_t* stage, int sub, int i) __attribute__((always_inline)) {
-    if (i < 4)
-      A[buf][i] = operand(stage, a_row[i], sub);
-    else
-      B[buf][i - 4] = operand(stage + kTileElems, b_row[i - 4], sub);
-  };
-  auto mfma = [&](int cur, int k) __attribute__((always_inline)) {
+  for (int mb = 0; mb < kMB; mb++) B[0][mb] = operand(lds, b_off[0], mb);
+
+  // MFMA k of a sub-step: block (nb, mb) = (k / kMB, k % kMB), W-major, so W
+  // operand nb is free after MFMA kMB nb + kMB - 1.
+  auto mfma = [&](int u, int k) __attribute__((always_inline)) {
     const int nb = k / kMB, mb = k % kMB;
-    acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[cur][nb], B[cur][mb], acc[nb][mb],
-                                                          0, 0, 0);
+    acc[nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[nb], B[u][mb], acc[nb][mb], 0, 0, 0);
   };
-  constexpr int kMfmaSub = 4 * kMB;   // MFMAs per 16-deep sub-step
-  constexpr int kOps = 4 + kMB;       // operand reads per sub-step
-  static_assert(kMfmaSub >= 2 * kLoadsTile, "one load per MFMA of the last sub-step");
-  static_assert(kMfmaSub >= kOps + 2, "reads interleave with MFMAs");
-  read_ops(0, lds, 0);
+  // Reads of sub-step u' (from stage) after MFMA k: x operand k/2 at even k
+  // < 2 kMB, W operand nb after the last MFMA of nb.
+  auto reads_after = [&](int k, const uint16_t* stage, int u2) __attribute__((always_inline)) {
+    if (k < 2 * kMB && (k & 1) == 0) B[u2][k >> 1] = operand(stage, b_off[u2], k >> 1);
+    if (k % kMB == kMB - 1) A[k / kMB] = operand(stage, a_off[u2], k / kMB);
+  };
 
   for (int t = 0; t < steps; t++) {
     const uint16_t* cur_stage = lds + (t & 1) * kStageElems;
-    // Sub-steps 0..2: multiply sub-step s, one operand read of sub-step
-    // s + 1 after each of its first MFMAs (the schedule is pinned: left to
-    // itself the compiler moves the reads to the end of the sub-step).
+    const uint16_t* next_stage = lds + ((t + 1) & 1) * kStageElems;
+    // Sub-step 0, reading sub-step 1's operands from the same stage.
 #pragma unroll
-    for (int s = 0; s < 3; s++) {
-#pragma unroll
-      for (int k = 0; k < kMfmaSub; k++) {
-        mfma(s & 1, k);
-        if (k < kOps) read_op((s & 1) ^ 1, cur_stage, s + 1, k);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int k = 0; k < kMfmaSub; k++) {
+      mfma(0, k);
+      reads_after(k, cur_stage, 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
     // This wave has read stage t & 1 and its loads of step t + 1 have landed;
     // after the barrier the same holds for every wave.
     __builtin_amdgcn_s_waitcnt(kPWaitAll);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    // Sub-step 3 (operands already in registers), one load of step t + 2 into
-    // the stage just freed after each MFMA, and halfway the sub-step 0
-    // operands of step t + 1. Past the last step the loads repeat the last
-    // step and the reads pick up the other stage: in bounds, never used.
+    // Sub-step 1, one load of step t + 2 into the stage just freed after every
+    // second MFMA, and the reads of step t + 1's sub-step 0. Past the last
+    // step the loads repeat the last step and the reads pick up the other
+    // stage: in bounds, never used.
     const int t_load = min(t + 2, steps - 1);
 #pragma unroll
     for (int k = 0; k < kMfmaSub; k++) {
       mfma(1, k);
-      if (wave < 4) {
-        dma(t_load, t & 1, 2 * k);
-        dma(t_load, t & 1, 2 * k + 1);
-      }
-      if (k >= 2 && k < 2 + kOps) read_op(0, lds + ((t + 1) & 1) * kStageElems, 0, k - 2);
+      if (wave < 4 && (k & 1)) dma(t_load, t & 1, k >> 1);
+      reads_after(k, next_stage, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   __builtin_amdgcn_s_waitcnt(kPWaitVmcnt0);
   // Every wave is past its last LDS read and its loads have landed: the ring
-  // is free for the output transpose.
+  // is free for the epilogue rows.
   __syncthreads();
 
-  // ---- epilogue: lane (li, hh) holds token m0 + 64mq + 32mb + li, channels
-  // 32nb + 8g + 4hh + e of the head in register 4g + e of acc[nb][mb], i.e.
-  // half (hh) of each 8-channel chunk c = 4nb + g.
+  // ---- epilogue. Accumulator (nb, mb) of lane (g, lr): channels
+  // 16nb + 4g .. +3 of token m0 + 64mq + 16mb + lr.
   uint16_t* out = part == 0 ? a.q_out : part == 1 ? a.k_out : a.v_out;
   const bool norm = !kPlain && part < 2;
-  const uint16_t* gamma = part == 0 ? a.q_gamma : a.k_gamma;
-  constexpr int hl = kHl;
-  constexpr int half = 8 * kHl;            // rot / 2
-  // Output transpose: the wave's 32 x 128 block goes through its own 8 KiB of
-  // LDS, written as 8-byte slots (2c + hh) ^ li of row li (conflict-free), and
-  // read back 16 bytes per lane as whole rows, so each global store writes
-  // 1 KiB contiguous (4 rows of the head-major output) instead of 16-byte
-  // pieces of 32 rows.
+  constexpr bool kFull = kHl == 8;          // rot == 128
+  constexpr int kHalf = 8 * kHl;            // rot / 2
+  // The prologue's row layout: lane j of 8-lane group rg holds chunks
+  // (chunk_a, chunk_b) of row rg, each RoPE pair (p, p + rot/2) in one lane.
+  const int j = lane & 7, rg = lane >> 3;
+  const bool pair_lane = kFull || j < kHl;
+  const int chunk_a = pair_lane ? j : 2 * kHl + 2 * (j - kHl);
+  const int chunk_b = pair_lane ? j + kHl : chunk_a + 1;
+  float gam[16];
+  if (norm) {
+    const uint16_t* gsrc = part == 0 ? a.q_gamma : a.k_gamma;
+    unpack8(*reinterpret_cast<const u32x4*>(gsrc + 8 * chunk_a), gam);
+    unpack8(*reinterpret_cast<const u32x4*>(gsrc + 8 * chunk_b), gam + 8);
+  }
+  // The wave's 32-row x 128-channel staging block.
   uint16_t* blk = lds + wave * (32 * kHD);
-  auto put = [&](int c, uint32_t w0, uint32_t w1) __attribute__((always_inline)) {
-    const u32x2 v2 = {w0, w1};
-    *reinterpret_cast<u32x2*>(blk + li * kHD + (((2 * c + hh) ^ li) * 4)) = v2;
-  };
 #pragma unroll
-  for (int mb = 0; mb < kMB; mb++) {
-    const int mrow0 = m0 + kTokWave * mq + 32 * mb;   // first row of the block (wave-uniform)
+  for (int mp = 0; mp < kMB / 2; mp++) {
+    const int mrow0 = m0 + kTokWave * mq + 32 * mp;   // first row of the block (wave-uniform)
     if (mrow0 >= a.seq_pad) continue;
-    const int m = mrow0 + li;
-    const bool valid = m < a.seq_len;
-    // bf16 GEMM result of this lane's half-chunks, packed: xb[c][0..1].
-    uint32_t xb[16][2];
+    // bf16 GEMM result -> rows: row 16h + lr, 8-byte slot 4nb + g.
 #pragma unroll
-    for (int c = 0; c < 16; c++) {
-      xb[c][0] = cvt_pk(acc[c >> 2][mb][4 * (c & 3)], acc[c >> 2][mb][4 * (c & 3) + 1]);
-      xb[c][1] = cvt_pk(acc[c >> 2][mb][4 * (c & 3) + 2], acc[c >> 2][mb][4 * (c & 3) + 3]);
-    }
-    if (!norm) {
+    for (int h = 0; h < 2; h++)
 #pragma unroll
-      for (int c = 0; c < 16; c++) put(c, valid ? xb[c][0] : 0u, valid ? xb[c][1] : 0u);
-    } else {
-      // Mean of squares in the prologue's order: per slot j an fma chain over
-      // chunk a then chunk b, channel order within a chunk, then ((s0+s7)+(s2+s5))
-      // + ((s1+s6)+(s3+s4)). The lower half-wave runs slots 0..3, the upper
-      // slots 4..7: permlane32_swap(x, y) leaves the lower half-wave's word of x
-      // in [0] and the lower half-wave's word of y in [0]'s upper lanes, the
-      // upper half-wave's words in [1], so with x = chunk c of slot j and y =
-      // chunk c' of slot j + 4 every lane gets channels 0..3 of its chunk in
-      // [0] and 4..7 in [1] -- one swap per word for both half-waves.
-      auto pair_sq = [&](int c, int c2, float acc_s) __attribute__((always_inline)) {
-        const auto w0 = __builtin_amdgcn_permlane32_swap(xb[c][0], xb[c2][0], false, false);
-        const auto w1 = __builtin_amdgcn_permlane32_swap(xb[c][1], xb[c2][1], false, false);
-        const uint32_t wd[4] = {w0[0], w1[0], w0[1], w1[1]};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const float v0 = bf16_lo(wd[q]), v1 = bf16_hi(wd[q]);
-          acc_s = fmaf(v0, v0, acc_s);
-          acc_s = fmaf(v1, v1, acc_s);
-        }
-        return acc_s;
-      };
-      auto slot_a = [&](int j) { return j < hl ? j : 2 * hl + 2 * (j - hl); };
-      auto slot_b = [&](int j) { return j < hl ? j + hl : 2 * hl + 2 * (j - hl) + 1; };
-      float sj[8];
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        // This lane's slot: j (lower half-wave) or j + 4 (upper).
-        const float mine =
-            pair_sq(slot_b(j), slot_b(j + 4), pair_sq(slot_a(j), slot_a(j + 4), 0.f));
-        const auto both = __builtin_amdgcn_permlane32_swap(__float_as_uint(mine),
-                                                           __float_as_uint(mine), false, false);
-        sj[j] = __uint_as_float(both[0]);
-        sj[j + 4] = __uint_as_float(both[1]);
+      for (int nb = 0; nb < kNB; nb++) {
+        const f32x4& c = acc[nb][2 * mp + h];
+        const int r = 16 * h + lr;
+        const u32x2 v2 = {cvt_pk(c[0], c[1]), cvt_pk(c[2], c[3])};
+        *reinterpret_cast<u32x2*>(blk + r * kHD + (((4 * nb + g) ^ (2 * e_swz(r))) * 4)) = v2;
       }
-      const float tot = ((sj[0] + sj[7]) + (sj[2] + sj[5])) + ((sj[1] + sj[6]) + (sj[3] + sj[4]));
-      const float r = rsqrt_rounded(tot * (1.0f / kHD) + a.eps);
-      // Normalised values of this lane's half-chunk c: (x r) gamma.
-      auto norm4 = [&](int c, float y[4]) __attribute__((always_inline)) {
-        const u32x2 g2 = *reinterpret_cast<const u32x2*>(gamma + 8 * c + 4 * hh);
+    // Rows back in the row layout, 8 rows per pass.
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const uint32_t xw = xb[c][e >> 1], gw = g2[e >> 1];
-          const float xv = (e & 1) ? bf16_hi(xw) : bf16_lo(xw);
-          const float gv = (e & 1) ? bf16_hi(gw) : bf16_lo(gw);
-          y[e] = (xv * r) * gv;
-        }
-      };
-      auto store4 = [&](int c, const float o[4]) __attribute__((always_inline)) {
-        put(c, valid ? cvt_pk(o[0], o[1]) : 0u, valid ? cvt_pk(o[2], o[3]) : 0u);
-      };
-      // Table row of this token (row 0 for padding rows, whose output is zero).
-      const int64_t trow = (int64_t)(valid ? m : 0) * half;
+    for (int pass = 0; pass < 4; pass++) {
+      const int r = 8 * pass + rg, m = mrow0 + r;
+      const u32x4 ca = *reinterpret_cast<const u32x4*>(blk + r * kHD + ((chunk_a ^ e_swz(r)) * 8));
+      const u32x4 cb = *reinterpret_cast<const u32x4*>(blk + r * kHD + ((chunk_b ^ e_swz(r)) * 8));
+      const bool valid = m < a.seq_len;
+      u32x4 oa = {0u, 0u, 0u, 0u}, ob = {0u, 0u, 0u, 0u};
+      if (valid) {
+        if (norm) {
+          // This lane's pairs 8j .. 8j + 7 (pair lanes) from token m's table row.
+          RopeEntry tab[8];
+          if (pair_lane) {
+            if (kMode == H3HIP_ROUND_REFERENCE) {
+              const u32x4* tp = reinterpret_cast<const u32x4*>(
+                  static_cast<const uint16_t*>(a.table) + ((int64_t)m * kHalf + 8 * j) * 4);
 #pragma unroll
-      for (int c = 0; c < hl; c++) {
-        // Pairs p = 8c + 4hh + e rotate channels p (chunk c) and p + rot/2
-        // (chunk c + hl), both in this lane.
-        RopeEntry te[4];
-        if (kMode == H3HIP_ROUND_REFERENCE) {
-          const u32x4* tp = reinterpret_cast<const u32x4*>(
-              static_cast<const uint16_t*>(a.table) + (trow + 8 * c + 4 * hh) * 4);
-          const u32x4 t01 = tp[0], t23 = tp[1];   // (c, -s, s, c) bf16 of pairs e
+              for (int q = 0; q < 4; q++) {
+                const u32x4 tv = tp[q];   // (c, -s, s, c) bf16 of pairs 2q, 2q + 1
+                tab[2 * q] = RopeEntry{bf16_lo(tv[0]), bf16_lo(tv[1])};
+                tab[2 * q + 1] = RopeEntry{bf16_lo(tv[2]), bf16_lo(tv[3])};
+              }
+            } else {
+              const f32x4* tp = reinterpret_cast<const f32x4*>(a.table) + (int64_t)m * kHalf + 8 * j;
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const u32x4& tv = e < 2 ? t01 : t23;
-            const int o = 2 * (e & 1);
-            te[e] = RopeEntry{bf16_lo(tv[o]), bf16_lo(tv[o + 1])};
+              for (int e = 0; e < 8; e++) {
+                const f32x4 tv = tp[e];
+                tab[e] = RopeEntry{tv[0], tv[2]};
+              }
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) tab[e] = RopeEntry{1.f, 0.f};
           }
+          float xv[16];
+          unpack8(ca, xv);
+          unpack8(cb, xv + 8);
+          norm_rope<kMode, kFull>(xv, gam, pair_lane, tab, a.eps, oa, ob);
         } else {
-          const f32x4* tp = reinterpret_cast<const f32x4*>(a.table) + trow + 8 * c + 4 * hh;
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const f32x4 tv = tp[e];
-            te[e] = RopeEntry{tv[0], tv[2]};
-          }
+          oa = ca;
+          ob = cb;
         }
-        float ya[4], yb[4], oa[4], ob[4];
-        norm4(c, ya);
-        norm4(c + hl, yb);
-#pragma unroll
-        for (int e = 0; e < 4; e++) rope_pair<kMode>(ya[e], yb[e], te[e], true, oa[e], ob[e]);
-        store4(c, oa);
-        store4(c + hl, ob);
       }
-      // Channels >= rot pass through (bf16-rounded as in the prologue).
-#pragma unroll
-      for (int c = 2 * hl; c < 16; c++) {
-        float y[4], o[4];
-        norm4(c, y);
-        rope_pair<kMode>(y[0], y[1], RopeEntry{1.f, 0.f}, false, o[0], o[1]);
-        rope_pair<kMode>(y[2], y[3], RopeEntry{1.f, 0.f}, false, o[2], o[3]);
-        store4(c, o);
+      if (m < a.seq_pad) {
+        uint16_t* dst = out + ((int64_t)head * a.seq_pad + m) * kHD;
+        *reinterpret_cast<u32x4*>(dst + 8 * chunk_a) = oa;
+        *reinterpret_cast<u32x4*>(dst + 8 * chunk_b) = ob;
       }
-    }
-    // Row r = 4i + lane / 16, chunk k = lane % 16: slots 2k, 2k + 1 sit at
-    // (2k ^ r) and (2k + 1) ^ r, i.e. the 16-byte word at 2k ^ (r & 30) with
-    // its halves swapped when r is odd.
-    uint16_t* dst = out + ((int64_t)head * a.seq_pad + mrow0) * kHD;
-    const int k = lane & 15;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int r = 4 * i + (lane >> 4);
-      u32x4 v = *reinterpret_cast<const u32x4*>(blk + r * kHD + ((2 * k) ^ (r & 30)) * 4);
-      if (r & 1) v = u32x4{v[2], v[3], v[0], v[1]};
-      if (mrow0 + r < a.seq_pad) *reinterpret_cast<u32x4*>(dst + r * kHD + 8 * k) = v;
     }
   }
 }
