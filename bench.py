@@ -33,15 +33,32 @@ FLOP_PER_TILE_HEAD = 4 * 128 ** 3   # QK^T and PV over one 128x128 tile, head_di
 C_HIDDEN = 5120               # the benchmark configs' model width (input of the QKV projection)
 
 
-def read_traffic(name: str):
-    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if any."""
+def read_profile_value(name: str, key: str):
+    """A `key: value` figure from a committed rocprofv3 summary, if any."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(key + ":"):
             return float(line.split(":", 1)[1])
     return None
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if any."""
+    return read_profile_value(name, "traffic_bytes_per_launch")
+
+
+def useful_tile_flops(plan_rows, seq_len: int, heads: int, tile: int = 128, d: int = 128):
+    """FLOPs of the active tiles without their padding: 4 * d * (query rows <
+    seq_len) * (key columns < seq_len) summed over the tiles, times heads."""
+    row_ptr, col_idx = plan_rows
+    total = 0
+    for qt in range(len(row_ptr) - 1):
+        rows = min(tile, seq_len - qt * tile)
+        cols = sum(min(tile, seq_len - int(kt) * tile) for kt in col_idx[row_ptr[qt]:row_ptr[qt + 1]])
+        total += rows * cols
+    return 4 * d * total * heads
 
 
 def interleaved_medians(fns: dict, reps: int = 12, warmup: int = 2) -> dict:
@@ -120,6 +137,34 @@ def cpu_baseline(shape, plan_rows, seconds: float = 12.0):
     n_heads = int(max(1, min(shape.heads - 1, math.ceil(seconds / max(first, 1e-3)) - 1)))
     dt = first + sum(one_head() for _ in range(n_heads))
     n_heads += 1
+
+    # Config 1 in full (all 4 heads, every row) through the same restatement.
+    from h3hip import configs as C
+    c1 = C.CFG1
+    bm1 = O.tile_bitmap(O.Rule(**c1.oracle_rule_kwargs()))
+    q1 = rng.standard_normal((c1.heads, c1.seq_len, D), dtype=np.float32)
+    k1 = rng.standard_normal((c1.heads, c1.seq_len, D), dtype=np.float32)
+    v1 = rng.standard_normal((c1.heads, c1.seq_len, D), dtype=np.float32)
+    t0 = time.perf_counter()
+    O.attend_masked(q1, k1, v1, 1.0 / math.sqrt(D), bm1, tile=128, threads=threads)
+    dt1 = time.perf_counter() - t0
+    flops1 = int(bm1.sum()) * c1.heads * 4 * 128 ** 2 * D
+
+    # The prologue on the host, in full at config 5's size (Q and K, every
+    # token and head), through the oracle's restatement in reference rounding.
+    inner = shape.heads * D
+    pos = O.positions_grid(shape.prefix_len, shape.frames, shape.height, shape.width)
+    ax, inv = O.rope_pairs_axes(1.0e4, 32, 48, 48)
+    gam = O.uniform_bf16((D,), 3, 0.9, 1.1)
+    t_pro = 0.0
+    for seed in (1, 2):
+        x = O.randn_bf16((S, inner), seed)
+        t0 = time.perf_counter()
+        O.qk_norm_rope(x, inner, S, shape.seq_pad, shape.heads, D, gam, 1e-6, pos, ax, inv,
+                       128, threads=threads)
+        t_pro += time.perf_counter() - t0
+        del x
+    pro_bytes = 2 * S * inner * 2 + 2 * shape.seq_pad * inner * 2 + S * 12 + 2 * D * 2
     return {
         "value": round(n_heads * head_flops / dt / 1e12, 6),
         "unit": "TFLOP/s",
@@ -134,6 +179,13 @@ def cpu_baseline(shape, plan_rows, seconds: float = 12.0):
                    f"the {shape.heads} heads of config 3 in {dt:.1f} s; value = active-tile "
                    f"FLOPs of those heads / time; a full layer would take "
                    f"{dt / n_heads * shape.heads:.0f} s"),
+        "cfg1_full": {"seconds": round(dt1, 3),
+                      "tflops_active": round(flops1 / dt1 / 1e12, 6),
+                      "sample": "config 1 (4 heads x 4,096 rows, band rule) in full"},
+        "prologue_cfg5_full": {"seconds": round(t_pro, 3),
+                               "gbps": round(pro_bytes / t_pro / 1e9, 2),
+                               "sample": ("Q and K of config 5 (31,885 tokens x 40 heads) in "
+                                          "full, reference rounding")},
     }
 
 
@@ -323,6 +375,8 @@ def main() -> int:
     plan = h3hip.TilePlan(shape.mask_rule(), heads=H)
     tile_build_ms = min(tile_build_ms, (time.perf_counter() - t0) * 1e3)
     attn_flops = plan.nnz * H * FLOP_PER_TILE_HEAD
+    attn_useful_flops = useful_tile_flops(plan.tiles(), S, H)
+    clk = read_profile_value("bsattn_fwd_cfg3_clock.txt", "effective_clock_ghz")
 
     # ---- synthetic inputs, resident in HBM ----------------------------------
     g = torch.Generator(device=dev)
@@ -409,6 +463,15 @@ def main() -> int:
         "attn_tflop_per_launch": round(attn_flops / 1e12, 4),
         "attn_tflops_active": round(attn_tflops, 3),
         "attn_mfma_peak_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+        # The same rate against the dense bf16 peak at the clock the chip holds
+        # under this kernel (cycles per XCD from GRBM_GUI_ACTIVE over the
+        # unprofiled duration, committed profile), beside the spec figure.
+        "attn_effective_clock_ghz": clk,
+        "attn_mfma_peak_frac_at_effective_clock": (
+            round(attn_tflops / (PEAK_BF16_TFLOPS * clk / 2.4), 4) if clk else None),
+        # Without the padding rows and columns inside the active tiles.
+        "attn_useful_tflop_per_launch": round(attn_useful_flops / 1e12, 4),
+        "attn_useful_tflops": round(attn_useful_flops / (attn_ms * 1e-3) / 1e12, 3),
         "prologue_qk_ms": round(pro_ms, 4),
         "prologue_qk_gbps": round(pro_gbps, 1),
         "ms_per_layer": round(pro_ms + attn_ms, 4),
