@@ -166,9 +166,10 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
     return *reinterpret_cast<const bf16x8*>(stage + off + blk * 16 * kPK);
   };
 
-  // HBM -> LDS: wave w moves rows 32w .. 32w+31 of the W tile and of the x
-  // tile, 8 rows per instruction (lane l: row 32w + 8i + l/8, chunk position
-  // l%8 filled from the global chunk the swizzle places there).
+  // HBM -> LDS by one wave per SIMD: loading wave lw (waves 0-3) moves rows
+  // 32 lw .. 32 lw + 31 and 32 (lw + 4) .. + 31 of the W tile and of the x
+  // tile, 8 rows per instruction (lane l: row + 8i + l/8, chunk position l%8
+  // filled from the global chunk the swizzle places there).
   const i32x4p w_rsrc = proj_rsrc(a.w, (uint32_t)(3 * inner) * (uint32_t)a.ldw * 2u);
   const i32x4p x_rsrc = proj_rsrc(a.x, (uint32_t)((a.seq_len - 1) * a.ldx + a.hidden) * 2u);
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(proj_lds_address(lds));
