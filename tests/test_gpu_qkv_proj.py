@@ -95,6 +95,10 @@ def _run(orc, S, hidden, H, rot, rounding, h3_tables=False, ldx=None, seed=7, ld
     (130, 128, 6, 96, 1, True),       # S just past one 128-row tile, rot 96 fp32 rounding
     (1000, 5120, 4, 128, 0, False),   # the benchmark configs' hidden width
     (700, 5376, 56, 96, 0, True),     # the H3 model: hidden 5,376, 56 heads, rot 96
+    (200, 64, 2, 128, 0, False),      # one reduction step (no second stage loaded up front)
+    (260, 192, 2, 128, 0, False),     # three steps: the last step's stage is the first's
+    (129, 320, 4, 96, 1, True),       # five steps, S one row past a tile, fp32 rounding
+    (1, 128, 2, 128, 0, False),       # a single token: one valid row in the last tile
 ])
 def test_fused_equals_prologue_of_plain(h3, orc, S, hidden, H, rot, rounding, h3t):
     x, w, plain, fused, (want_q, want_k) = _run(orc, S, hidden, H, rot, rounding, h3t)
