@@ -35,10 +35,12 @@
 // the prologue's own entry function. The output therefore equals
 // h3hip_qk_norm_rope applied to this kernel's bf16 GEMM result, bit for bit.
 // Rows are stored whole: 8 consecutive head-major rows (2 KiB) per pass.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
 #include "norm_rope.h"
+#include "tile_order.h"
 
 namespace h3hip {
 
@@ -68,8 +70,7 @@ constexpr int kNB = kHD / 16;                 // 16-channel accumulator blocks p
 constexpr int kRowsWave = kPM / kPWaves;      // rows of each operand tile a wave loads
 constexpr int kLoadsTile = kRowsWave / 8;     // 1 KiB loads per operand tile per wave
 constexpr int kLoadsStep = 4 * kLoadsTile;    // loads per step of a loading wave
-constexpr int kGroupM = 4;                // token tiles per launch-order group
-constexpr int kXcds = 8;
+constexpr int kXcds = kOrderXcds;
 constexpr int kTileElems = kPM * kPK;     // one operand tile (W or x) of a step
 constexpr int kStageElems = 2 * kTileElems;
 constexpr int kMfmaSub = kNB * kMB;       // MFMAs per 32-deep sub-step
@@ -133,22 +134,16 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   // row lr of an A block and column lr of a B block at k = 8g .. 8g + 7, and
   // rows 4g .. 4g + 3 of column lr of the 16 x 16 result.
   const int lr = lane & 15, g = lane >> 4;
-  // Tile order. Workgroup b runs on XCD b % 8 (round-robin dispatch) and
-  // XCD x takes the tiles [x q + min(x, r), ...) of a grouped order (total =
-  // 8 q + r), so the workgroups one XCD runs at once cover a compact block
-  // of kGroupM token tiles x a few channel tiles and share their x and W
-  // slices in that XCD's L2.
+  // Tile order (TileOrder). Workgroup b runs on XCD b % 8 (round-robin
+  // dispatch), as that XCD's (b / 8)-th workgroup; the grid is 8 x the longest
+  // XCD list, and a workgroup past its XCD's list has no tile.
   const int inner = a.heads * kHD;
   const int tiles_n = 3 * inner / kPN;
-  const int total = a.tiles_m * tiles_n;
+  const TileOrder order{a.tiles_m, tiles_n};
   const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
-  const int tile = xcd * (total / kXcds) + min(xcd, total % kXcds) + slot;
-  const int group = tile / (kGroupM * tiles_n);
-  const int first_m = group * kGroupM;
-  const int gm = min(a.tiles_m - first_m, kGroupM);
-  const int local = tile - group * kGroupM * tiles_n;
-  const int tm = first_m + local % gm, tn = local / gm;
-  const int m0 = tm * kPM, n0 = tn * kPN;
+  if (slot >= order.length(xcd)) return;
+  const int tile = order.tile(xcd, slot);
+  const int m0 = (tile >> 16) * kPM, n0 = (tile & 0xffff) * kPN;
   const int part = n0 / inner;                        // uniform over the tile
   const int head = (n0 - part * inner) / kHD + nh;    // this wave's head
 
@@ -414,7 +409,12 @@ extern "C" int h3hip_qkv_proj(const void* x, int64_t ldx, const void* w, int64_t
              static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out),
              static_cast<uint16_t*>(v_out), ldx, ldw, eps, hidden, rot, seq_len, seq_pad, heads,
              tiles_m};
-  const dim3 grid(tiles_m * (3 * heads * kHD / kPN));
+  // 8 x the longest XCD list of the tile order (a few empty workgroups when
+  // the lists differ in length).
+  const TileOrder order{tiles_m, 3 * heads * kHD / kPN};
+  int longest = 0;
+  for (int xcd = 0; xcd < kXcds; xcd++) longest = std::max(longest, order.length(xcd));
+  const dim3 grid(kXcds * longest);
   hipStream_t st = as_stream(stream);
   if (plain)
     qkv_proj_kernel<H3HIP_ROUND_REFERENCE, 8, true><<<grid, kPThreads, 0, st>>>(a);
