@@ -99,6 +99,12 @@ def _run(orc, S, hidden, H, rot, rounding, h3_tables=False, ldx=None, seed=7, ld
     (260, 192, 2, 128, 0, False),     # three steps: the last step's stage is the first's
     (129, 320, 4, 96, 1, True),       # five steps, S one row past a tile, fp32 rounding
     (1, 128, 2, 128, 0, False),       # a single token: one valid row in the last tile
+    # Launch order (tile_order.h): 6 x 3 tiles, XCD lists of 4,4,4,2,2,2,0,0 (a full
+    # chunk, short chunks of 2, two XCDs with no tile, 14 empty workgroups) ...
+    (1500, 256, 2, 128, 0, False),
+    # ... and 7 x 6 tiles, lists of 7,7,7,7,4,4,3,3 (full chunks and short chunks of 3
+    # on the same XCD).
+    (1700, 320, 4, 96, 1, True),
 ])
 def test_fused_equals_prologue_of_plain(h3, orc, S, hidden, H, rot, rounding, h3t):
     x, w, plain, fused, (want_q, want_k) = _run(orc, S, hidden, H, rot, rounding, h3t)
