@@ -12,7 +12,7 @@ One step = one DiT layer's hot path at config 3 (S = 31,885 -> 32,000,
 The tile plan is built once per shape (timed separately, not per layer).
 Inputs are synthetic and already resident in HBM when the timed region starts.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-extras]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 10] [--no-cpu-baseline] [--no-extras]
 """
 from __future__ import annotations
 
@@ -339,7 +339,7 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--only", choices=("attention", "prologue", "copy", "qkv"),
