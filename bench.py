@@ -202,6 +202,25 @@ def profile_only(args, env) -> int:
         torch.cuda.synchronize()
         print(f"copy: {args.steps} x {src.numel() * 2} bytes read and written")
         return 0
+    if args.only == "anchor":
+        fns, notes, plan, keep = sdpa_anchor_fns(dev)
+        names = [n for n in ("h3hip_bsattn_fwd", "torch_flash_aotriton") if n in fns]
+        for _ in range(args.warmup + args.steps):
+            for n in names:
+                fns[n]()
+        torch.cuda.synchronize()
+        print(f"anchor: {args.steps} launches each of {', '.join(names)} at [1, 40, 18176, 128]"
+              + (f"; {notes}" if notes else ""))
+        plan.close()
+        return 0
+    if args.only == "mfma_ceiling":
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        fns, _, keep = mfma_ceiling_fns(dev, cus)
+        for _ in range(args.warmup + args.steps):
+            fns["mfma32_random"]()
+        torch.cuda.synchronize()
+        print(f"mfma_ceiling: {args.steps} launches of the 32x32x16 stream on random operands")
+        return 0
     if args.only == "qkv":
         x, w = qkv_inputs(env)
         vh = torch.empty_like(env["qh"])
@@ -228,6 +247,199 @@ def profile_only(args, env) -> int:
     torch.cuda.synchronize()
     print(f"prologue: {args.steps} launches, Q and K [{S}, {inner}] -> [{H}, {S_pad}, {D}]")
     return 0
+
+
+def probe_lib():
+    """libch3probe.so: same-run hardware ceilings (MFMA stream, HBM streams),
+    built beside libch3hip.so and not part of the attention path."""
+    import ctypes
+    path = os.path.join(ROOT, "minimax-h3-swift_amd", "libch3probe.so")
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is not built; run __graft_entry__.build()")
+    L = ctypes.CDLL(path)
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    L.h3probe_mfma_operand_bytes.restype, L.h3probe_mfma_operand_bytes.argtypes = i64, [i32]
+    L.h3probe_mfma_flops.restype, L.h3probe_mfma_flops.argtypes = ctypes.c_double, [i32, i32]
+    L.h3probe_mfma.restype = ctypes.c_int
+    L.h3probe_mfma.argtypes = [i32, vp, i32, i32, vp, vp]
+    L.h3probe_stream.restype = ctypes.c_int
+    L.h3probe_stream.argtypes = [i32, vp, vp, i64, i32, i32, vp, vp]
+    return L
+
+
+def _stream_ptr():
+    import torch
+    return ctypes_ptr(torch.cuda.current_stream().cuda_stream)
+
+
+def ctypes_ptr(x):
+    import ctypes
+    return ctypes.c_void_p(int(x))
+
+
+def mfma_ceiling_fns(dev, cus: int, iters: int = 2000):
+    """Launchers of the sustained-MFMA probe (one workgroup of 8 waves per CU):
+    v_mfma_f32_32x32x16_bf16 (the attention kernel's shape) and
+    v_mfma_f32_16x16x32_bf16 (the projection's), on N(0,1) bf16 operands and on
+    zeros. Returns ({name: fn}, FLOPs per launch)."""
+    import torch
+    P = probe_lib()
+    n = P.h3probe_mfma_operand_bytes(cus) // 2
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    rnd = torch.randn(n, generator=g, device=dev).to(torch.bfloat16)
+    zero = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    sink = torch.empty(cus * 512, dtype=torch.float32, device=dev)
+
+    def mk(shape, ops):
+        def fn():
+            rc = P.h3probe_mfma(shape, ctypes_ptr(ops.data_ptr()), cus, iters,
+                                ctypes_ptr(sink.data_ptr()), _stream_ptr())
+            assert rc == 0, f"h3probe_mfma returned {rc}"
+        return fn
+    fns = {"mfma32_random": mk(0, rnd), "mfma32_zero": mk(0, zero),
+           "mfma16_random": mk(1, rnd)}
+    return fns, P.h3probe_mfma_flops(cus, iters), (rnd, zero, sink)
+
+
+def ceilings_extra(args, dev, cus: int, read_bytes: int, write_bytes: int):
+    """The chip's sustained MFMA rate per shape (power-limited at real data) and
+    the best HBM read-only, write-only and read+write streams of the prologue's
+    byte counts, swept over grid size and per-thread unroll, in this run."""
+    import torch
+    fns, flops, keep = mfma_ceiling_fns(dev, cus)
+    med = interleaved_medians(fns, reps=6, warmup=2)
+    res = {"timing": "medians of interleaved calls",
+           "mfma_probe": ("one workgroup of 8 waves per CU, 4 independent accumulator chains "
+                          "per wave, operands in registers, 2,000 iterations")}
+    for name, ms in med.items():
+        res[name + "_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+        res[name + "_peak_frac"] = round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+    del keep
+    P = probe_lib()
+    nbytes = max(read_bytes, write_bytes)
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+    sweep = [(b, u) for b in (1024, 2048, 4096, 8192) for u in (2, 4, 8)]
+
+    def mk(kind, nb, blocks, unroll):
+        def fn():
+            rc = P.h3probe_stream(kind, ctypes_ptr(src.data_ptr()), ctypes_ptr(dst.data_ptr()),
+                                  nb, blocks, unroll, ctypes_ptr(sink.data_ptr()), _stream_ptr())
+            assert rc == 0, f"h3probe_stream returned {rc}"
+        return fn
+    for kind, label, nb, moved in ((0, "read", read_bytes, read_bytes),
+                                   (1, "write", write_bytes, write_bytes),
+                                   (2, "copy", read_bytes, 2 * read_bytes)):
+        m = interleaved_medians({f"{b}x{u}": mk(kind, nb, b, u) for b, u in sweep},
+                                reps=8, warmup=2)
+        best = min(m, key=m.get)
+        res[f"{label}_stream"] = {"bytes": moved, "best_ms": round(m[best], 4),
+                                  "best_gbps": round(moved / (m[best] * 1e-3) / 1e9, 1),
+                                  "best_grid_x_unroll": best,
+                                  "worst_gbps": round(moved / (max(m.values()) * 1e-3) / 1e9, 1)}
+    rd, wr = res["read_stream"], res["write_stream"]
+    # Reads then writes of the prologue's bytes, each at its own best rate: a
+    # kernel that overlapped them perfectly could at best reach the copy's rate.
+    res["read_then_write_ms"] = round(rd["best_ms"] + wr["best_ms"], 4)
+    res["read_then_write_gbps"] = round((read_bytes + write_bytes)
+                                        / ((rd["best_ms"] + wr["best_ms"]) * 1e-3) / 1e9, 1)
+    del src, dst, sink
+    return res
+
+
+def sdpa_anchor_inputs(dev, heads: int = 40, seq: int = 18176):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(4321)
+    q, k, v = (torch.randn((1, heads, seq, 128), generator=g, device=dev).to(torch.bfloat16)
+               for _ in range(3))
+    return q, k, v
+
+
+def sdpa_anchor_fns(dev, heads: int = 40, seq: int = 18176):
+    """Dense attention at config 4's padded shape ([1, 40, 18,176, 128] bf16,
+    no mask, every tile active) through torch's fused SDPA kernels -- the
+    flash backend (AOTriton on this ROCm build, and CK where the build has it)
+    and the memory-efficient backend -- beside this library's kernel on a
+    dense plan of the same length. The math backend is never allowed, so a
+    backend that cannot run raises instead of falling back."""
+    import torch
+    import h3hip
+    from h3hip import ops
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    q, k, v = sdpa_anchor_inputs(dev, heads, seq)
+    out = torch.empty_like(q)
+    plan = h3hip.TilePlan(h3hip.MaskRule.dense(seq), heads=heads)
+    scale = 1.0 / math.sqrt(128)
+    fns, notes = {}, {}
+
+    def ours():
+        ops.bsattn_fwd(plan, q[0], k[0], v[0], scale, out=out[0])
+    fns["h3hip_bsattn_fwd"] = ours
+
+    def sdpa_with(backend, lib=None):
+        def fn():
+            if lib is not None:
+                torch.backends.cuda.preferred_rocm_fa_library(lib)
+            with sdpa_kernel([backend]):
+                torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=scale)
+        return fn
+    cands = [("torch_flash_aotriton", SDPBackend.FLASH_ATTENTION, "aotriton"),
+             ("torch_flash_ck", SDPBackend.FLASH_ATTENTION, "ck"),
+             ("torch_mem_efficient", SDPBackend.EFFICIENT_ATTENTION, None)]
+    for name, backend, lib in cands:
+        fn = sdpa_with(backend, lib)
+        try:
+            fn()
+            torch.cuda.synchronize()
+            fns[name] = fn
+        except Exception as e:  # a backend this build or GPU does not have
+            notes[name] = f"did not run: {type(e).__name__}: {str(e).splitlines()[0][:160]}"
+    try:
+        torch.backends.cuda.preferred_rocm_fa_library("default")
+    except Exception:
+        pass
+    return fns, notes, plan, (q, k, v, out)
+
+
+def sdpa_anchor_extra(args, dev):
+    """Same-run anchor for the attention kernel's roofline: dense attention at
+    config 4's padded shape through torch's fused SDPA backends, interleaved
+    with h3hip_bsattn_fwd on a dense plan, plus a max-abs difference of each
+    output from ours."""
+    import torch
+    fns, notes, plan, keep = sdpa_anchor_fns(dev)
+    q, k, v, out = keep
+    heads, seq = q.shape[1], q.shape[2]
+    flops = 4.0 * heads * seq * seq * 128
+    med = interleaved_medians(fns, reps=max(10, args.steps // 2), warmup=2)
+    res = {"timing": "medians of interleaved calls",
+           "shape": f"[1, {heads}, {seq}, 128] bf16, no mask (all {plan.nnz} tiles per head)",
+           "tflop_per_call": round(flops / 1e12, 4)}
+    fns["h3hip_bsattn_fwd"]()
+    ref = out.float()
+    for name, ms in med.items():
+        entry = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                 "peak_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+        if name != "h3hip_bsattn_fwd":
+            from torch.nn.attention import sdpa_kernel, SDPBackend
+            be = (SDPBackend.EFFICIENT_ATTENTION if "efficient" in name
+                  else SDPBackend.FLASH_ATTENTION)
+            if name == "torch_flash_ck":
+                torch.backends.cuda.preferred_rocm_fa_library("ck")
+            with sdpa_kernel([be]):
+                o = torch.nn.functional.scaled_dot_product_attention(
+                    q, k, v, scale=1.0 / math.sqrt(128))
+            torch.backends.cuda.preferred_rocm_fa_library("default")
+            entry["max_abs_diff_vs_h3hip"] = round(float((o.float() - ref).abs().max()), 5)
+            del o
+        res[name] = entry
+    res.update(notes)
+    plan.close()
+    del keep, ref
+    return res
 
 
 def qkv_inputs(env):
@@ -342,10 +554,14 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--only", choices=("attention", "prologue", "copy", "qkv"),
+    ap.add_argument("--only", choices=("attention", "prologue", "copy", "qkv", "anchor",
+                                       "mfma_ceiling"),
                     help="profiling mode: run one kernel --steps times at config 3 (prologue: "
                          "config 5, Q and K only; copy: a plain 1 GiB device copy for counter "
-                         "calibration; qkv: the fused QKV projection) and print nothing but a one-line summary")
+                         "calibration; qkv: the fused QKV projection; anchor: this library's "
+                         "attention and torch's flash SDPA alternately, dense, at config 4's "
+                         "padded shape; mfma_ceiling: the sustained 32x32x16 MFMA stream) and "
+                         "print nothing but a one-line summary")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -463,11 +679,13 @@ def main() -> int:
         "attn_tflop_per_launch": round(attn_flops / 1e12, 4),
         "attn_tflops_active": round(attn_tflops, 3),
         "attn_mfma_peak_frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-        # The same rate against the dense bf16 peak at the clock the chip holds
-        # under this kernel (cycles per XCD from GRBM_GUI_ACTIVE over the
-        # unprofiled duration, committed profile), beside the spec figure.
-        "attn_effective_clock_ghz": clk,
-        "attn_mfma_peak_frac_at_effective_clock": (
+        # The same rate against the dense bf16 peak at a clock NOT measured in
+        # this run: the committed profile's cycles per XCD (GRBM_GUI_ACTIVE)
+        # over its unprofiled duration, from an earlier run and possibly another
+        # box. Context only; the roofline fraction is against the spec peak.
+        "attn_profiled_clock_ghz": clk,
+        "attn_profiled_clock_source": "profiles/bsattn_fwd_cfg3_clock.txt (an earlier run)",
+        "attn_mfma_peak_frac_at_profiled_clock": (
             round(attn_tflops / (PEAK_BF16_TFLOPS * clk / 2.4), 4) if clk else None),
         # Without the padding rows and columns inside the active tiles.
         "attn_useful_tflop_per_launch": round(attn_useful_flops / 1e12, 4),
@@ -530,6 +748,10 @@ def main() -> int:
         result["prologue_relayout_ceiling_gbps"] = extras["cfg5_prologue_qk"]["relayout_ceiling_gbps"]
         result["prologue_copy_ceiling_gbps"] = extras["cfg5_prologue_qk"]["copy_ceiling_gbps"]
         del q_in, k_in, qk_in, qk_hm, copy_src, copy_dst
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        extras["ceilings"] = ceilings_extra(args, dev, cus, 2 * S * inner * 2,
+                                             2 * S_pad * inner * 2)
+        extras["cfg4_dense_anchor_torch_sdpa"] = sdpa_anchor_extra(args, dev)
         extras["cfg3_qkv_proj"] = qkv_projection_extra(args, env=locals())
         extras["cfg3_attention_layer"] = attention_layer_extra(args, env=locals())
         for name in ("cfg3_1344x768x5s_frame0", "cfg2_864x480x7s", "cfg4_dense_864x480x7s",
@@ -556,6 +778,10 @@ def main() -> int:
             del qq, kk, vv, oo
             p.close()
         result["extras"] = extras
+        # Against what the chip sustains for the kernel's MFMA shape on random
+        # operands, measured in this run (the ceilings extra).
+        c32 = extras["ceilings"]["mfma32_random_tflops"]
+        result["attn_frac_of_same_run_mfma_stream"] = round(attn_tflops / c32, 4)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(shape, plan.tiles())

@@ -1,0 +1,212 @@
+// Same-run hardware ceilings for bench.py: not part of the attention path and not
+// linked into libch3hip.so.
+//
+//  * h3probe_mfma: a sustained stream of one MFMA shape on every CU (8 waves per
+//    CU, operands in registers, no memory traffic inside the loop). Its rate on
+//    random bf16 operands is what the chip sustains for that shape under its
+//    power limit; on zero operands, close to the clock-limited rate.
+//  * h3probe_read / h3probe_write / h3probe_copy: HBM streams of a given byte
+//    count (read-only, write-only, read+write), with the grid and the per-thread
+//    unroll as parameters so bench.py can sweep them and keep the best.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 512;
+constexpr int kVar = 4;  // distinct operand registers per wave
+
+// Every wave keeps four independent accumulator chains busy; the chains'
+// operands rotate over kVar register sets so consecutive MFMAs read different
+// registers. `ops` holds 2 * kVar bf16x8 per thread of the grid.
+template <int kShape>
+__global__ __launch_bounds__(kThreads, 1) void mfma_stream(const bf16x8* __restrict__ ops,
+                                                           int iters, float* __restrict__ sink) {
+  const int gid = blockIdx.x * kThreads + threadIdx.x;
+  bf16x8 a[kVar], b[kVar];
+#pragma unroll
+  for (int v = 0; v < kVar; v++) {
+    a[v] = ops[gid * 2 * kVar + v];
+    b[v] = ops[gid * 2 * kVar + kVar + v];
+  }
+  float s = 0.f;
+  if (kShape == 0) {
+    f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int i = 0; i < iters; i++) {
+#pragma unroll
+      for (int v = 0; v < kVar; v++) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[v], b[v], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(v + 1) % kVar], b[v], c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[v], b[(v + 1) % kVar], c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(v + 2) % kVar], b[(v + 3) % kVar], c3,
+                                                     0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; j++) s += c0[j] + c1[j] + c2[j] + c3[j];
+  } else {
+    // Twice the instructions of half the FLOPs each: eight f32x4 chains.
+    f32x4 c[8] = {};
+    for (int i = 0; i < iters; i++) {
+#pragma unroll
+      for (int v = 0; v < kVar; v++)
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+          c[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[(v + k) % kVar],
+                                                         b[(v + (k >> 1)) % kVar], c[k], 0, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) s += c[k][0] + c[k][1] + c[k][2] + c[k][3];
+  }
+  // A data-dependent store the compiler cannot remove; it fires for no input
+  // bench.py passes (finite operands never sum to exactly this value).
+  if (s == 1234.5f) sink[gid] = s;
+}
+
+// Read-only stream: each thread XOR-folds kUnroll 16-byte chunks per grid
+// stride and writes one word per block.
+template <int kUnroll>
+__global__ __launch_bounds__(256) void read_stream(const u32x4* __restrict__ src, int64_t n,
+                                                   uint32_t* __restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * kUnroll;
+  uint32_t acc = 0;
+  for (int64_t base = (int64_t)blockIdx.x * 256 * kUnroll + threadIdx.x; base < n;
+       base += stride) {
+    u32x4 x[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      const int64_t i = base + (int64_t)u * 256;
+      x[u] = i < n ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) acc ^= x[u][0] ^ x[u][1] ^ x[u][2] ^ x[u][3];
+  }
+  __shared__ uint32_t red[256];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = 0;
+    for (int i = 0; i < 256; i++) r ^= red[i];
+    sink[blockIdx.x] = r;
+  }
+}
+
+// Write-only stream of a constant pattern.
+template <int kUnroll>
+__global__ __launch_bounds__(256) void write_stream(u32x4* __restrict__ dst, int64_t n,
+                                                    uint32_t pattern) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * kUnroll;
+  const u32x4 w = {pattern, pattern, pattern, pattern};
+  for (int64_t base = (int64_t)blockIdx.x * 256 * kUnroll + threadIdx.x; base < n;
+       base += stride) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      const int64_t i = base + (int64_t)u * 256;
+      if (i < n) __builtin_nontemporal_store(w, dst + i);
+    }
+  }
+}
+
+// Read+write stream: a plain copy.
+template <int kUnroll>
+__global__ __launch_bounds__(256) void copy_stream(const u32x4* __restrict__ src,
+                                                   u32x4* __restrict__ dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * kUnroll;
+  for (int64_t base = (int64_t)blockIdx.x * 256 * kUnroll + threadIdx.x; base < n;
+       base += stride) {
+    u32x4 x[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      const int64_t i = base + (int64_t)u * 256;
+      x[u] = i < n ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+      const int64_t i = base + (int64_t)u * 256;
+      if (i < n) __builtin_nontemporal_store(x[u], dst + i);
+    }
+  }
+}
+
+int launch_status() {
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Operand buffer size in bytes for `blocks` workgroups.
+int64_t h3probe_mfma_operand_bytes(int32_t blocks) {
+  return (int64_t)blocks * kThreads * 2 * kVar * 16;
+}
+
+// FLOPs of one h3probe_mfma launch (both shapes do the same FLOPs per iteration).
+double h3probe_mfma_flops(int32_t blocks, int32_t iters) {
+  return (double)blocks * (kThreads / 64) * iters * kVar * 4 * 32768.0;
+}
+
+// shape 0: v_mfma_f32_32x32x16_bf16, 1: v_mfma_f32_16x16x32_bf16. `ops` holds
+// h3probe_mfma_operand_bytes(blocks) bytes, `sink` blocks * 512 floats.
+// Returns 0, -1 on a bad argument, -2 on a launch failure.
+int h3probe_mfma(int32_t shape, const void* ops, int32_t blocks, int32_t iters, void* sink,
+                 void* stream) {
+  if ((shape != 0 && shape != 1) || !ops || !sink || blocks <= 0 || iters <= 0) return -1;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // 96 KiB of dynamic LDS keeps one workgroup per CU, as in the attention kernel.
+  const int lds = 96 * 1024;
+  if (shape == 0) {
+    if (hipFuncSetAttribute((const void*)mfma_stream<0>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+      return -2;
+    mfma_stream<0><<<blocks, kThreads, lds, s>>>(static_cast<const bf16x8*>(ops), iters,
+                                                 static_cast<float*>(sink));
+  } else {
+    if (hipFuncSetAttribute((const void*)mfma_stream<1>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+      return -2;
+    mfma_stream<1><<<blocks, kThreads, lds, s>>>(static_cast<const bf16x8*>(ops), iters,
+                                                 static_cast<float*>(sink));
+  }
+  return launch_status();
+}
+
+// kind 0: read `bytes` from src (sink: blocks words); 1: write `bytes` to dst;
+// 2: copy `bytes` from src to dst. bytes a multiple of 16, buffers 16-byte
+// aligned; unroll 1, 2, 4 or 8; blocks of 256 threads.
+int h3probe_stream(int32_t kind, const void* src, void* dst, int64_t bytes, int32_t blocks,
+                   int32_t unroll, void* sink, void* stream) {
+  if (bytes <= 0 || bytes % 16 || blocks <= 0) return -1;
+  if (unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8) return -1;
+  if ((kind == 0 || kind == 2) && (!src || (reinterpret_cast<uintptr_t>(src) & 15))) return -1;
+  if ((kind == 1 || kind == 2) && (!dst || (reinterpret_cast<uintptr_t>(dst) & 15))) return -1;
+  if (kind == 0 && !sink) return -1;
+  if (kind < 0 || kind > 2) return -1;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t n = bytes / 16;
+  const u32x4* in = static_cast<const u32x4*>(src);
+  u32x4* out = static_cast<u32x4*>(dst);
+  uint32_t* sk = static_cast<uint32_t*>(sink);
+#define H3PROBE_DISPATCH(U)                                                   \
+  case U:                                                                     \
+    if (kind == 0) read_stream<U><<<blocks, 256, 0, s>>>(in, n, sk);          \
+    else if (kind == 1) write_stream<U><<<blocks, 256, 0, s>>>(out, n, 0x3f803f80u); \
+    else copy_stream<U><<<blocks, 256, 0, s>>>(in, out, n);                   \
+    break;
+  switch (unroll) {
+    H3PROBE_DISPATCH(1)
+    H3PROBE_DISPATCH(2)
+    H3PROBE_DISPATCH(4)
+    H3PROBE_DISPATCH(8)
+  }
+#undef H3PROBE_DISPATCH
+  return launch_status();
+}
+
+}  // extern "C"

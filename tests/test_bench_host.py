@@ -53,3 +53,16 @@ def test_useful_flops_sparse_against_token_count():
     tok = np.minimum(128, S - 128 * np.arange(n))           # valid rows per tile
     pairs = sum(int(tok[q]) * int(tok[k]) for q in range(n) for k in range(n) if bm[q, k])
     assert bench.useful_tile_flops((row_ptr, col_idx), S, heads=3) == 4 * 128 * pairs * 3
+
+
+def test_probe_library_loads_and_counts():
+    """libch3probe.so (bench.py's same-run ceilings) loads on the host and its
+    host-side bookkeeping matches the probe's loop: 8 waves x 4 chains x 4
+    operand sets x 32,768 FLOP per 32x32x16 MFMA per iteration."""
+    P = bench.probe_lib()
+    assert P.h3probe_mfma_operand_bytes(256) == 256 * 512 * 8 * 16
+    assert P.h3probe_mfma_flops(256, 2000) == 256 * 8 * 2000 * 4 * 4 * 32768.0
+    # Argument checks refuse before touching the GPU.
+    assert P.h3probe_mfma(2, None, 1, 1, None, None) == -1
+    assert P.h3probe_stream(0, None, None, 17, 1, 4, None, None) == -1
+    assert P.h3probe_stream(1, None, None, 16, 1, 3, None, None) == -1
