@@ -159,14 +159,22 @@ int h3hip_mask_from_rule(const h3hip_mask_rule* rule, uint8_t* d_bitmap, void* s
 /* h3hip_mask_from_rule without any allocation. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * The rule's flag tables (BAND global columns, landmark frames) and the host
- * lists they come from are staged in a static per-GPU scratch array of
- * 192 KiB inside the library, instead of a temporary allocation: at most
- * 32,768 flags (tile columns or frames) and 32,768 listed entries, larger
- * rules are refused with H3HIP_EINVAL. Same bitmap as h3hip_mask_from_rule.
+ * The rule's flag tables (BAND global columns, landmark frames) are built in a
+ * static per-GPU scratch array of 192 KiB inside the library instead of a
+ * temporary allocation: at most 32,768 flags (tile columns or frames) and
+ * 32,768 listed entries; larger rules are refused with H3HIP_EINVAL. Same
+ * bitmap as h3hip_mask_from_rule.
+ * Lists of up to 256 entries (global columns or landmark frames) travel by
+ * value in the kernel arguments: nothing is copied from host memory and
+ * nothing synchronises, so DENSE, BAND, LOCAL and AXIAL rules with such lists
+ * can be captured into a HIP graph and replayed (the host lists may be freed
+ * after the call). Longer lists are staged from host memory and `stream` is
+ * synchronised before returning; BITMAP rules copy the host bitmap and
+ * synchronise. Under stream capture both of those are refused with
+ * H3HIP_EINVAL and capture is left intact.
  * Every call on one GPU shares that GPU's scratch: calls that overlap on one
- * GPU (concurrent streams or threads) race. Synchronises `stream` when it
- * staged a host list. */
+ * GPU (concurrent streams or threads, or replays of graphs holding this call)
+ * race. */
 int h3hip_mask_from_rule_noalloc(const h3hip_mask_rule* rule, uint8_t* d_bitmap, void* stream);
 
 /* Block mask -> CSR on the device. d_bitmap [nq * nk] bytes; d_row_ptr[nq + 1]

@@ -291,6 +291,21 @@ __global__ __launch_bounds__(256) void flags_from_list_kernel(uint8_t* flags, in
   for (int32_t i = threadIdx.x; i < n_list; i += 256) flags[list[i]] = 1;
 }
 
+// The same with the list passed by value in the kernel arguments, so nothing
+// is staged from host memory: the form h3hip_mask_from_rule_noalloc uses for
+// short lists, which keeps it capturable into a HIP graph.
+constexpr int32_t kArgList = 256;
+struct ListArg {
+  int32_t n;
+  int32_t v[kArgList];
+};
+__global__ __launch_bounds__(256) void flags_from_arg_kernel(uint8_t* flags, int32_t n_flags,
+                                                             ListArg list) {
+  for (int32_t i = threadIdx.x; i < n_flags; i += 256) flags[i] = 0;
+  __syncthreads();
+  for (int32_t i = threadIdx.x; i < list.n; i += 256) flags[list.v[i]] = 1;
+}
+
 static int csr_on_device(const uint8_t* d_bitmap, int32_t nq, int32_t nk, int32_t* d_row_ptr,
                          hipStream_t stream, int64_t* nnz) {
   row_count_kernel<<<nq, 256, 0, stream>>>(d_bitmap, nk, d_row_ptr);
@@ -341,10 +356,19 @@ int h3hip_mask_from_rule_noalloc(const h3hip_mask_rule* rule, uint8_t* d_bitmap,
   if (rc) return rc;
   H3_REQUIRE(d_bitmap != nullptr, H3HIP_EINVAL, "d_bitmap is NULL");
   hipStream_t st = as_stream(stream);
+  // Under stream capture nothing may be staged from host memory: the copy would
+  // re-read the caller's host array at every replay, and the synchronisation
+  // that keeps that array alive is illegal while capturing.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  H3_HIP_CHECK(hipStreamIsCapturing(st, &cap));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
   const int32_t n_tiles = (rule->seq_len + H3HIP_TILE - 1) / H3HIP_TILE;
   if (rule->kind == H3HIP_RULE_BITMAP) {
+    H3_REQUIRE(!capturing, H3HIP_EINVAL,
+               "a BITMAP rule copies the host bitmap and cannot run under stream capture");
     H3_HIP_CHECK(hipMemcpyAsync(d_bitmap, rule->bitmap, (size_t)n_tiles * n_tiles,
                                 hipMemcpyHostToDevice, st));
+    H3_HIP_CHECK(hipStreamSynchronize(st));
     return H3HIP_OK;
   }
   const bool band = rule->kind == H3HIP_RULE_BAND;
@@ -358,6 +382,11 @@ int h3hip_mask_from_rule_noalloc(const h3hip_mask_rule* rule, uint8_t* d_bitmap,
   H3_REQUIRE(n_list <= kScratchList, H3HIP_EINVAL,
              "%d listed %s exceed the static scratch's %d entries", n_list,
              band ? "global columns" : "landmarks", kScratchList);
+  const bool by_value = n_list <= kArgList;
+  H3_REQUIRE(by_value || !capturing, H3HIP_EINVAL,
+             "%d listed %s exceed the %d that travel in kernel arguments; longer lists are "
+             "staged from host memory and cannot run under stream capture",
+             n_list, band ? "global columns" : "landmarks", kArgList);
   RuleDev dev{rule->kind, rule->seq_len, rule->prefix_len, rule->frames, rule->height,
               rule->width, rule->frame_window, rule->spatial_tile_h, rule->spatial_tile_w,
               rule->spatial_window, rule->band, n_tiles, nullptr, nullptr};
@@ -367,14 +396,21 @@ int h3hip_mask_from_rule_noalloc(const h3hip_mask_rule* rule, uint8_t* d_bitmap,
     rc = scratch_on_current_device(&sp);
     if (rc) return rc;
     uint8_t* flags = band ? sp : sp + kScratchFlags;
-    int32_t* list = reinterpret_cast<int32_t*>(sp + 2 * kScratchFlags);
-    if (n_list > 0) {
+    if (by_value) {
+      ListArg arg{};
+      arg.n = n_list;
+      const int32_t* src = band ? rule->global_cols : rule->landmark_frames;
+      for (int32_t i = 0; i < n_list; i++) arg.v[i] = src[i];
+      flags_from_arg_kernel<<<1, 256, 0, st>>>(flags, n_flags, arg);
+      rc = check_launch("flags_from_arg_kernel");
+    } else {
+      int32_t* list = reinterpret_cast<int32_t*>(sp + 2 * kScratchFlags);
       H3_HIP_CHECK(hipMemcpyAsync(list, band ? rule->global_cols : rule->landmark_frames,
                                   sizeof(int32_t) * n_list, hipMemcpyHostToDevice, st));
       staged = true;
+      flags_from_list_kernel<<<1, 256, 0, st>>>(flags, n_flags, list, n_list);
+      rc = check_launch("flags_from_list_kernel");
     }
-    flags_from_list_kernel<<<1, 256, 0, st>>>(flags, n_flags, list, n_list);
-    rc = check_launch("flags_from_list_kernel");
     if (rc) return rc;
     if (band) dev.col_global = flags;
     else dev.frame_landmark = flags;
@@ -382,8 +418,7 @@ int h3hip_mask_from_rule_noalloc(const h3hip_mask_rule* rule, uint8_t* d_bitmap,
   mask_rule_kernel<<<dim3(n_tiles, n_tiles), 256, 0, st>>>(dev, d_bitmap);
   rc = check_launch("mask_rule_kernel");
   if (rc) return rc;
-  // The rule's host lists were staged asynchronously: keep them alive until the
-  // copy has consumed them.
+  // A list staged from host memory must outlive the copy that consumes it.
   if (staged) H3_HIP_CHECK(hipStreamSynchronize(st));
   return H3HIP_OK;
 }
