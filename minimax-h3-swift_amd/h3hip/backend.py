@@ -220,11 +220,12 @@ def sampling_activation_bytes(packed_tokens: int, materialises_scores: bool = Tr
 
 def h3hip_resident_bytes(seq_len: int, heads: int, blocks: int, nnz: int, n_tiles: int,
                          head_dim: int = 128) -> int:
-    """What the sparse backend itself keeps resident for a render: one
-    token-major bf16 output [S, heads*head_dim] per block (each consumed inside
-    its sampling step's graph) and the plan's device lists -- row_ptr, col_idx
-    and the persistent schedule, int32. Linear in S; no [S, S] term."""
-    outputs = blocks * seq_len * heads * head_dim * 2
+    """What the sparse backend itself keeps resident for a render: two
+    token-major bf16 outputs [S, heads*head_dim] per block, used alternately
+    by the block's successive calls (each consumed inside its sampling step's
+    graph), and the plan's device lists -- row_ptr, col_idx and the persistent
+    schedule, int32. Linear in S; no [S, S] term."""
+    outputs = 2 * blocks * seq_len * heads * head_dim * 2
     lists = 4 * (n_tiles + 1 + nnz + heads * n_tiles + 257)
     return outputs + lists
 

@@ -84,7 +84,7 @@ def test_axial_density_at_the_production_shape(orc):
 def test_memory_plan_drops_the_quadratic_term(h3):
     """MemoryPlan.swift:105-118: a backend that never materialises scores removes
     the quadratic term; at H3's S = 15,731 that is 7.2 GB of the 32.3 GB estimate,
-    and the backend's own residents (50 block outputs, the plan) stay linear."""
+    and the backend's own residents (two outputs per block for 50 blocks, the plan) stay linear."""
     from h3hip.backend import H3HIPBackend, SDPABackend, h3hip_resident_bytes, \
         sampling_activation_bytes
     S = 15731
@@ -95,4 +95,4 @@ def test_memory_plan_drops_the_quadratic_term(h3):
     # The reference's fitted point: 53.1 GB at S = 20,392 with the dense backend.
     assert abs(sampling_activation_bytes(20392) / 1e9 - 44.7) < 0.1
     res = h3hip_resident_bytes(S, 56, 50, nnz=10815, n_tiles=123)
-    assert res < 12e9 and h3hip_resident_bytes(2 * S, 56, 50, 10815, 246) < 2.01 * res
+    assert res < 24e9 and h3hip_resident_bytes(2 * S, 56, 50, 10815, 246) < 2.01 * res
