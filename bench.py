@@ -264,6 +264,8 @@ def probe_lib():
     L.h3probe_mfma.argtypes = [i32, vp, i32, i32, vp, vp]
     L.h3probe_stream.restype = ctypes.c_int
     L.h3probe_stream.argtypes = [i32, vp, vp, i64, i32, i32, vp, vp]
+    L.h3probe_relayout.restype = ctypes.c_int
+    L.h3probe_relayout.argtypes = [i32, vp, vp, i32, i32, i32, vp]
     return L
 
 
@@ -302,10 +304,18 @@ def mfma_ceiling_fns(dev, cus: int, iters: int = 2000):
     return fns, P.h3probe_mfma_flops(cus, iters), (rnd, zero, sink)
 
 
-def ceilings_extra(args, dev, cus: int, read_bytes: int, write_bytes: int):
-    """The chip's sustained MFMA rate per shape (power-limited at real data) and
+RELAYOUT_VARIANTS = {0: "tokens-fastest 8x5x512", 1: "tokens-fastest 2x5x256",
+                     2: "tokens-fastest 4x4x256", 3: "heads-fastest 4x4x256",
+                     4: "2x2 blocks 4x5x512"}
+
+
+def ceilings_extra(args, dev, cus: int, read_bytes: int, write_bytes: int, relayout=None):
+    """The chip's sustained MFMA rate per shape (power-limited at real data),
     the best HBM read-only, write-only and read+write streams of the prologue's
-    byte counts, swept over grid size and per-thread unroll, in this run."""
+    byte counts, swept over grid size and per-thread unroll, and the best of
+    several thread mappings of the prologue's layout change alone (token-major
+    Q|K -> head-major, no arithmetic; relayout = (rows, rows_pad, heads)), in
+    this run."""
     import torch
     fns, flops, keep = mfma_ceiling_fns(dev, cus)
     med = interleaved_medians(fns, reps=6, warmup=2)
@@ -339,6 +349,26 @@ def ceilings_extra(args, dev, cus: int, read_bytes: int, write_bytes: int):
                                   "best_gbps": round(moved / (m[best] * 1e-3) / 1e9, 1),
                                   "best_grid_x_unroll": best,
                                   "worst_gbps": round(moved / (max(m.values()) * 1e-3) / 1e9, 1)}
+    if relayout is not None:
+        rows, rows_pad, heads = relayout
+        rin = src[:rows * heads * 128]
+        rout = dst[:heads * rows_pad * 128]
+
+        def mkr(v):
+            def fn():
+                rc = P.h3probe_relayout(v, ctypes_ptr(rin.data_ptr()), ctypes_ptr(rout.data_ptr()),
+                                        rows, rows_pad, heads, _stream_ptr())
+                assert rc == 0, f"h3probe_relayout returned {rc}"
+            return fn
+        m = interleaved_medians({RELAYOUT_VARIANTS[v]: mkr(v) for v in RELAYOUT_VARIANTS},
+                                reps=8, warmup=2)
+        moved = (rows + rows_pad) * heads * 256
+        best = min(m, key=m.get)
+        res["relayout_stream"] = {"bytes": moved, "best_ms": round(m[best], 4),
+                                  "best_gbps": round(moved / (m[best] * 1e-3) / 1e9, 1),
+                                  "best_mapping": best,
+                                  "by_mapping_gbps": {k: round(moved / (v * 1e-3) / 1e9, 1)
+                                                      for k, v in m.items()}}
     rd, wr = res["read_stream"], res["write_stream"]
     # Reads then writes of the prologue's bytes, each at its own best rate: a
     # kernel that overlapped them perfectly could at best reach the copy's rate.
@@ -497,10 +527,12 @@ def qkv_projection_extra(args, env):
 
 def attention_layer_extra(args, env):
     """AttentionLayer.callAsFunction (DiTBlock.swift:336-359) at config 3, end to
-    end: QKV projection + Q/K norm/RoPE, block-sparse attention, out-projection
-    (a plain GEMM, hipBLASLt via torch.mm in both paths). Two paths for the
-    first part: the fused projection kernel, or hipBLASLt's GEMM followed by
-    the prologue kernel (V then read in place from the token-major qkv)."""
+    end: QKV projection + Q/K norm/RoPE, block-sparse attention, out-projection.
+    Three paths: every kernel this library's (fused projection, attention,
+    h3hip_out_proj); the fused projection with hipBLASLt's out-projection
+    (torch.mm); and hipBLASLt's GEMMs with the prologue kernel between them
+    (V then read in place from the token-major qkv). The out-projection alone
+    is timed both ways beside them."""
     import numpy as np
     import torch
     from h3hip import ops
@@ -520,6 +552,12 @@ def attention_layer_extra(args, env):
     table = ops.rope_table(env["pos"], env["ax"], env["inv"])
     eps = env["C"].QK_EPS
 
+    def all_h3hip_path():
+        ops.qkv_proj(x, w, env["gq"], env["gk"], table, heads=H, eps=eps, seq_pad=S_pad,
+                     out=(qh, kh, vh))
+        ops.bsattn_fwd_strided(plan, qh, kh, vh, scale, out=att_view)
+        ops.out_proj(att, w_out, out=y)
+
     def fused_path():
         ops.qkv_proj(x, w, env["gq"], env["gk"], table, heads=H, eps=eps, seq_pad=S_pad,
                      out=(qh, kh, vh))
@@ -534,15 +572,30 @@ def attention_layer_extra(args, env):
         ops.bsattn_fwd_strided(plan, qh, kh, v_view, scale, out=att_view)
         torch.mm(att, w_out.t(), out=y)
 
-    med = interleaved_medians({"fused_qkv": fused_path, "hipblaslt_qkv": unfused_path},
+    def out_h3hip():
+        ops.out_proj(att, w_out, out=y)
+
+    def out_hipblaslt():
+        torch.mm(att, w_out.t(), out=y)
+
+    med = interleaved_medians({"all_h3hip": all_h3hip_path, "fused_qkv": fused_path,
+                               "hipblaslt_qkv": unfused_path, "out_proj_h3hip": out_h3hip,
+                               "out_proj_hipblaslt": out_hipblaslt},
                               reps=max(12, args.steps))
-    res = {"timing": "medians of interleaved calls"}
+    res = {"timing": "medians of interleaved calls",
+           "paths": {"all_h3hip": "fused QKV projection + attention + out-projection, all this "
+                                  "library's kernels",
+                     "fused_qkv": "fused QKV projection + attention + hipBLASLt out-projection",
+                     "hipblaslt_qkv": "hipBLASLt QKV GEMM + prologue + attention + hipBLASLt "
+                                      "out-projection"}}
     for name, ms in med.items():
         res[name + "_ms"] = round(ms, 4)
-    flops = (2.0 * S * C_HIDDEN * 3 * inner + plan.nnz * H * FLOP_PER_TILE_HEAD
-             + 2.0 * S * inner * C_HIDDEN)
+    out_flops = 2.0 * S * inner * C_HIDDEN
+    res["out_proj_h3hip_tflops"] = round(out_flops / (med["out_proj_h3hip"] * 1e-3) / 1e12, 1)
+    res["out_proj_hipblaslt_tflops"] = round(out_flops / (med["out_proj_hipblaslt"] * 1e-3) / 1e12, 1)
+    flops = (2.0 * S * C_HIDDEN * 3 * inner + plan.nnz * H * FLOP_PER_TILE_HEAD + out_flops)
     res["layer_tflop"] = round(flops / 1e12, 4)
-    best = min(res["fused_qkv_ms"], res["hipblaslt_qkv_ms"])
+    best = min(res["all_h3hip_ms"], res["fused_qkv_ms"], res["hipblaslt_qkv_ms"])
     res["best_tflops"] = round(flops / (best * 1e-3) / 1e12, 1)
     return res
 
@@ -750,7 +803,11 @@ def main() -> int:
         del q_in, k_in, qk_in, qk_hm, copy_src, copy_dst
         cus = torch.cuda.get_device_properties(dev).multi_processor_count
         extras["ceilings"] = ceilings_extra(args, dev, cus, 2 * S * inner * 2,
-                                             2 * S_pad * inner * 2)
+                                             2 * S_pad * inner * 2, relayout=(S, S_pad, 2 * H))
+        extras["cfg5_prologue_qk"]["frac_of_best_relayout_stream"] = round(
+            extras["cfg5_prologue_qk"]["gbps"] / extras["ceilings"]["relayout_stream"]["best_gbps"], 4)
+        extras["cfg5_prologue_qk"]["frac_of_best_copy_stream"] = round(
+            extras["cfg5_prologue_qk"]["gbps"] / extras["ceilings"]["copy_stream"]["best_gbps"], 4)
         extras["cfg4_dense_anchor_torch_sdpa"] = sdpa_anchor_extra(args, dev)
         extras["cfg3_qkv_proj"] = qkv_projection_extra(args, env=locals())
         extras["cfg3_attention_layer"] = attention_layer_extra(args, env=locals())

@@ -255,6 +255,20 @@ int h3hip_qkv_proj(const void* x, int64_t ldx, const void* w, int64_t ldw, int32
                    int32_t heads, int32_t head_dim, void* q_out, void* k_out, void* v_out,
                    void* stream);
 
+/* The out-projection of AttentionLayer.callAsFunction (DiTBlock.swift:359:
+ * matmul(merged, outWeight.T), no bias): y = x . w^T in bf16 with fp32
+ * accumulation, on the same MFMA main loop as h3hip_qkv_proj, written
+ * token-major.
+ *   x: device bf16 [seq_len, in_features] (the attention output, token-major
+ *      [S, heads*head_dim]), row stride ldx elements.
+ *   w: device bf16 [out_features, in_features] (outWeight), row stride ldw.
+ *   y: device bf16 [seq_len, out_features], row stride ldy; rows < seq_len
+ *      written.
+ * Declines unless in_features is a multiple of 64 and out_features a
+ * multiple of 256. */
+int h3hip_out_proj(const void* x, int64_t ldx, const void* w, int64_t ldw, int32_t in_features,
+                   int32_t out_features, int32_t seq_len, void* y, int64_t ldy, void* stream);
+
 /* -------------------------------------------------------------- attention */
 
 /* Block-sparse attention over the plan's active tiles: for each query row,

@@ -56,6 +56,10 @@ struct ProjArgs {
   int64_t ldx, ldw;
   float eps;
   int32_t hidden, rot, seq_len, seq_pad, heads, tiles_m;
+  // Out-projection mode: n_out output channels, written token-major into
+  // q_out with row stride ldo.
+  int32_t n_out;
+  int64_t ldo;
 };
 
 constexpr int kPM = 256;                  // tokens per workgroup
@@ -122,8 +126,10 @@ __device__ __forceinline__ uint32_t proj_lds_address(const uint16_t* p) {
 }
 
 // kHl = rot / 16 (8-channel chunks per rotation half); kPlain: write the bf16
-// GEMM result of every part unchanged (the materialised qkv, for tests).
-template <int kMode, int kHl, bool kPlain>
+// GEMM result of every part unchanged (the materialised qkv, for tests);
+// kOut: the out-projection, a plain GEMM of n_out channels written
+// token-major [seq_len, n_out] (row stride ldo) instead of head-major parts.
+template <int kMode, int kHl, bool kPlain, bool kOut = false>
 __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStageElems];   // 128 KiB
 
@@ -138,14 +144,15 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   // dispatch), as that XCD's (b / 8)-th workgroup; the grid is 8 x the longest
   // XCD list, and a workgroup past its XCD's list has no tile.
   const int inner = a.heads * kHD;
-  const int tiles_n = 3 * inner / kPN;
+  const int n_total = kOut ? a.n_out : 3 * inner;
+  const int tiles_n = n_total / kPN;
   const TileOrder order{a.tiles_m, tiles_n};
   const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds;
   if (slot >= order.length(xcd)) return;
   const int tile = order.tile(xcd, slot);
   const int m0 = (tile >> 16) * kPM, n0 = (tile & 0xffff) * kPN;
-  const int part = n0 / inner;                        // uniform over the tile
-  const int head = (n0 - part * inner) / kHD + nh;    // this wave's head
+  const int part = kOut ? 0 : n0 / inner;                   // uniform over the tile
+  const int head = kOut ? 0 : (n0 - part * inner) / kHD + nh;   // this wave's head
 
   // Operand offsets within a stage (elements). A block nb = W row
   // nh*128 + 16nb + lr, B block mb = x row 64mq + 16mb + lr; sub-step u reads
@@ -165,7 +172,7 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   // 32 lw .. 32 lw + 31 and 32 (lw + 4) .. + 31 of the W tile and of the x
   // tile, 8 rows per instruction (lane l: row + 8i + l/8, chunk position l%8
   // filled from the global chunk the swizzle places there).
-  const i32x4p w_rsrc = proj_rsrc(a.w, (uint32_t)(3 * inner) * (uint32_t)a.ldw * 2u);
+  const i32x4p w_rsrc = proj_rsrc(a.w, (uint32_t)n_total * (uint32_t)a.ldw * 2u);
   const i32x4p x_rsrc = proj_rsrc(a.x, (uint32_t)((a.seq_len - 1) * a.ldx + a.hidden) * 2u);
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(proj_lds_address(lds));
   const int lw = wave & 3;   // loading wave: rows of waves lw and lw + 4
@@ -278,7 +285,7 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   // ---- epilogue. Accumulator (nb, mb) of lane (g, lr): channels
   // 16nb + 4g .. +3 of token m0 + 64mq + 16mb + lr.
   uint16_t* out = part == 0 ? a.q_out : part == 1 ? a.k_out : a.v_out;
-  const bool norm = !kPlain && part < 2;
+  const bool norm = !kPlain && !kOut && part < 2;
   constexpr bool kFull = kHl == 8;          // rot == 128
   constexpr int kHalf = 8 * kHl;            // rot / 2
   // The prologue's row layout: lane j of 8-lane group rg holds chunks
@@ -352,7 +359,14 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
           ob = cb;
         }
       }
-      if (m < a.seq_pad) {
+      if (kOut) {
+        // Token-major: row m's 256 bytes of channels n0 + 128 nh .. + 127.
+        if (valid) {
+          uint16_t* dst = a.q_out + (int64_t)m * a.ldo + n0 + nh * kHD;
+          *reinterpret_cast<u32x4*>(dst + 8 * chunk_a) = oa;
+          *reinterpret_cast<u32x4*>(dst + 8 * chunk_b) = ob;
+        }
+      } else if (m < a.seq_pad) {
         uint16_t* dst = out + ((int64_t)head * a.seq_pad + m) * kHD;
         *reinterpret_cast<u32x4*>(dst + 8 * chunk_a) = oa;
         *reinterpret_cast<u32x4*>(dst + 8 * chunk_b) = ob;
@@ -408,7 +422,7 @@ extern "C" int h3hip_qkv_proj(const void* x, int64_t ldx, const void* w, int64_t
              rope_table,
              static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_out),
              static_cast<uint16_t*>(v_out), ldx, ldw, eps, hidden, rot, seq_len, seq_pad, heads,
-             tiles_m};
+             tiles_m, 0, 0};
   // 8 x the longest XCD list of the tile order (a few empty workgroups when
   // the lists differ in length).
   const TileOrder order{tiles_m, 3 * heads * kHD / kPN};
@@ -427,4 +441,38 @@ extern "C" int h3hip_qkv_proj(const void* x, int64_t ldx, const void* w, int64_t
   else
     qkv_proj_kernel<H3HIP_ROUND_FP32, 6, false><<<grid, kPThreads, 0, st>>>(a);
   return check_launch("qkv_proj_kernel");
+}
+
+extern "C" int h3hip_out_proj(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                              int32_t in_features, int32_t out_features, int32_t seq_len,
+                              void* y, int64_t ldy, void* stream) {
+  H3_REQUIRE(in_features > 0 && out_features > 0 && seq_len > 0, H3HIP_EINVAL,
+             "bad shape: in_features %d out_features %d seq_len %d", in_features, out_features,
+             seq_len);
+  if (in_features % kPK != 0 || out_features % kPN != 0) {
+    set_error("declined: in_features %d / out_features %d (needs multiples of 64 and 256)",
+              in_features, out_features);
+    return H3HIP_DECLINED;
+  }
+  H3_REQUIRE(x && w && y, H3HIP_EINVAL, "NULL tensor argument");
+  H3_REQUIRE(ldx >= in_features && ldx % 8 == 0 && ldw >= in_features && ldw % 8 == 0 &&
+                 ldy >= out_features && ldy % 8 == 0,
+             H3HIP_EINVAL, "ldx %lld / ldw %lld / ldy %lld must cover a row and be multiples of 8",
+             (long long)ldx, (long long)ldw, (long long)ldy);
+  const int tiles_m = (seq_len + kPM - 1) / kPM;
+  H3_REQUIRE((int64_t)tiles_m * kPM * ldx * 2 < ((int64_t)1 << 31) &&
+                 (int64_t)out_features * ldw * 2 < ((int64_t)1 << 31),
+             H3HIP_EINVAL, "x or W exceeds 2 GiB (32-bit buffer offsets)");
+  auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  H3_REQUIRE(aligned16(x) && aligned16(w) && aligned16(y), H3HIP_EINVAL,
+             "tensors must be 16-byte aligned");
+  ProjArgs a{static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), nullptr, nullptr,
+             nullptr, static_cast<uint16_t*>(y), nullptr, nullptr, ldx, ldw, 0.f, in_features,
+             128, seq_len, tiles_m * kPM, 1, tiles_m, out_features, ldy};
+  const TileOrder order{tiles_m, out_features / kPN};
+  int longest = 0;
+  for (int xcd = 0; xcd < kXcds; xcd++) longest = std::max(longest, order.length(xcd));
+  qkv_proj_kernel<H3HIP_ROUND_REFERENCE, 8, true, true>
+      <<<dim3(kXcds * longest), kPThreads, 0, as_stream(stream)>>>(a);
+  return check_launch("qkv_proj_kernel (out-projection)");
 }

@@ -108,6 +108,8 @@ SIGNATURES = {
                                       _vp, _vp, ctypes.c_float, _vp, ctypes.c_int32,
                                       ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                       ctypes.c_int32, ctypes.c_int32, _vp, _vp, _vp, _vp]),
+    "h3hip_out_proj": (ctypes.c_int, [_vp, ctypes.c_int64, _vp, ctypes.c_int64, ctypes.c_int32,
+                                      ctypes.c_int32, ctypes.c_int32, _vp, ctypes.c_int64, _vp]),
     "h3hip_bsattn_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32,
                                         ctypes.c_float, _vp, ctypes.c_int32, _vp]),
     "h3hip_bsattn_fwd_strided": (ctypes.c_int, [_vp, ctypes.POINTER(ViewC),

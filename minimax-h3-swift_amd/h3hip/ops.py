@@ -231,6 +231,31 @@ def qkv_proj(x: torch.Tensor, w: torch.Tensor, q_gamma: torch.Tensor | None = No
     return q_out, k_out, v_out
 
 
+def out_proj(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None):
+    """Out-projection y = x . w^T (DiTBlock.swift:359, matmul(merged,
+    outWeight.T)): x [S, in_features] bf16 (the attention's token-major
+    output), w [out_features, in_features] bf16; returns y [S, out_features]
+    bf16 (or writes ``out``, any row stride), or None when declined."""
+    _require_gpu_bf16("x", x)
+    _require_gpu_bf16("w", w)
+    if x.dim() != 2 or w.dim() != 2 or x.stride(1) != 1 or w.stride(1) != 1:
+        raise ValueError("x and w must be 2-D with unit column stride")
+    S, fin = x.shape
+    if w.shape[1] != fin:
+        raise ValueError(f"w must be [out_features, {fin}], got {tuple(w.shape)}")
+    fout = w.shape[0]
+    if out is None:
+        out = torch.empty((S, fout), dtype=torch.bfloat16, device=x.device)
+    elif (out.dim() != 2 or out.shape != (S, fout) or out.stride(1) != 1
+          or out.dtype != torch.bfloat16 or not out.is_cuda):
+        raise ValueError(f"out must be a bf16 GPU [{S}, {fout}] view with unit column stride")
+    rc = L.lib().h3hip_out_proj(_ptr(x), x.stride(0), _ptr(w), w.stride(0), fin, fout, S,
+                                _ptr(out), out.stride(0), _stream(x))
+    if L.check(rc, allow_declined=True) == L.DECLINED:
+        return None
+    return out
+
+
 # -------------------------------------------------------------------- attention
 
 def _head_major_qkv(plan: TilePlan, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):

@@ -5,9 +5,11 @@
 //    CU, operands in registers, no memory traffic inside the loop). Its rate on
 //    random bf16 operands is what the chip sustains for that shape under its
 //    power limit; on zero operands, close to the clock-limited rate.
-//  * h3probe_read / h3probe_write / h3probe_copy: HBM streams of a given byte
-//    count (read-only, write-only, read+write), with the grid and the per-thread
-//    unroll as parameters so bench.py can sweep them and keep the best.
+//  * h3probe_stream: HBM streams of a given byte count (read-only, write-only,
+//    read+write), with the grid and the per-thread unroll as parameters so
+//    bench.py can sweep them and keep the best.
+//  * h3probe_relayout: the prologue's token-major -> head-major layout change
+//    without arithmetic, in several thread mappings.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -134,6 +136,53 @@ __global__ __launch_bounds__(256) void copy_stream(const u32x4* __restrict__ src
   }
 }
 
+// Token-major [rows, heads * 128] -> head-major [heads, rows_pad, 128] (bf16):
+// the prologue's layout change with no arithmetic. 16 lanes per 256-byte row
+// (one 16-byte chunk each). kMap 0: consecutive row groups take consecutive
+// tokens of one head (contiguous writes); 1: consecutive heads of one token
+// (contiguous reads); 2: a wave's four rows are 2 tokens x 2 heads. kTok
+// tokens per workgroup, kU rows in flight per thread; tokens >= rows are
+// written as zeros.
+template <int kTok, int kU, int kThr, int kMap>
+__global__ __launch_bounds__(kThr) void relayout_stream(const u32x4* __restrict__ in,
+                                                       u32x4* __restrict__ out, int rows,
+                                                       int rows_pad, int heads) {
+  constexpr int kG = kThr / 16;
+  const int g = threadIdx.x >> 4, c = threadIdx.x & 15;
+  const int s0 = blockIdx.x * kTok;
+  const int total = kTok * heads;
+  for (int p0 = 0; p0 < total; p0 += kU * kG) {
+    u32x4 x[kU];
+    int tok[kU], hd[kU];
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+      const int r = p0 + u * kG + g;
+      if (kMap == 0) {
+        hd[u] = r / kTok;
+        tok[u] = r % kTok;
+      } else if (kMap == 1) {
+        tok[u] = r / heads;
+        hd[u] = r % heads;
+      } else {
+        const int blk = r >> 2, q = r & 3;
+        tok[u] = 2 * (blk % (kTok / 2)) + (q & 1);
+        hd[u] = 2 * (blk / (kTok / 2)) + (q >> 1);
+      }
+      const int s = s0 + tok[u];
+      x[u] = (r < total && s < rows && hd[u] < heads)
+                 ? __builtin_nontemporal_load(in + ((int64_t)s * heads + hd[u]) * 16 + c)
+                 : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+      const int r = p0 + u * kG + g;
+      const int s = s0 + tok[u];
+      if (r < total && s < rows_pad && hd[u] < heads)
+        __builtin_nontemporal_store(x[u], out + ((int64_t)hd[u] * rows_pad + s) * 16 + c);
+    }
+  }
+}
+
 int launch_status() {
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
@@ -206,6 +255,30 @@ int h3probe_stream(int32_t kind, const void* src, void* dst, int64_t bytes, int3
     H3PROBE_DISPATCH(8)
   }
 #undef H3PROBE_DISPATCH
+  return launch_status();
+}
+
+// The prologue's relayout without arithmetic: in [rows, heads * 128] bf16
+// token-major, out [heads, rows_pad, 128] head-major (rows_pad a multiple of
+// 8). variant: 0 tokens-fastest 8 tokens x 5 rows in flight x 512 threads,
+// 1 tokens-fastest 2 x 5 x 256, 2 tokens-fastest 4 x 4 x 256, 3 heads-fastest
+// 4 x 4 x 256, 4 2x2 blocks 4 x 5 x 512.
+int h3probe_relayout(int32_t variant, const void* in, void* out, int32_t rows, int32_t rows_pad,
+                     int32_t heads, void* stream) {
+  if (!in || !out || rows <= 0 || rows_pad < rows || rows_pad % 8 || heads <= 0 || heads % 2)
+    return -1;
+  if ((reinterpret_cast<uintptr_t>(in) & 15) || (reinterpret_cast<uintptr_t>(out) & 15)) return -1;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const u32x4* i4 = static_cast<const u32x4*>(in);
+  u32x4* o4 = static_cast<u32x4*>(out);
+  switch (variant) {
+    case 0: relayout_stream<8, 5, 512, 0><<<rows_pad / 8, 512, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    case 1: relayout_stream<2, 5, 256, 0><<<rows_pad / 2, 256, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    case 2: relayout_stream<4, 4, 256, 0><<<rows_pad / 4, 256, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    case 3: relayout_stream<4, 4, 256, 1><<<rows_pad / 4, 256, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    case 4: relayout_stream<4, 5, 512, 2><<<rows_pad / 4, 512, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    default: return -1;
+  }
   return launch_status();
 }
 
