@@ -12,8 +12,10 @@ with the projection and the norm/RoPE either fused in one kernel
 (h3hip_qkv_proj) or run as hipBLASLt's GEMM followed by the prologue kernel
 (h3hip_qk_norm_rope), the attention through the backend seam (block-sparse
 kernel with a context, the reference's dense SDPA otherwise), and the
-out-projection -- a plain GEMM -- on hipBLASLt. Q and K come out head-major and
-V is read in place, so no relayout copy runs between the stages.
+out-projection -- a plain GEMM -- on the projection kernel's main loop
+(h3hip_out_proj), or on hipBLASLt when that kernel declines the shape. Q and K
+come out head-major and V is read in place, so no relayout copy runs between
+the stages.
 """
 from __future__ import annotations
 
@@ -145,4 +147,7 @@ class AttentionLayer:
             raise NotImplementedError(
                 f"no kernel takes head_dim {self.head_dim} / rot {rope.rot} / heads {self.heads}")
         merged = self._attend(*qkv, context)
-        return torch.mm(merged, self.out_weight.t())
+        y = ops.out_proj(merged, self.out_weight)
+        if y is None:       # a width the kernel declines: hipBLASLt's GEMM
+            y = torch.mm(merged, self.out_weight.t())
+        return y
