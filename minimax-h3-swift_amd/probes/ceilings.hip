@@ -52,6 +52,42 @@ __global__ __launch_bounds__(kThreads, 1) void mfma_stream(const bf16x8* __restr
     }
 #pragma unroll
     for (int j = 0; j < 16; j++) s += c0[j] + c1[j] + c2[j] + c3[j];
+  } else if (kShape == 2) {
+    // The same stream with the accumulators in the AGPR file: the MFMA is
+    // written out so its C/D operands are tied to AGPRs.
+    f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int i = 0; i < iters; i++) {
+#pragma unroll
+      for (int v = 0; v < kVar; v++) {
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c0) : "v"(a[v]), "v"(b[v]));
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                     : "+a"(c1) : "v"(a[(v + 1) % kVar]), "v"(b[v]));
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                     : "+a"(c2) : "v"(a[v]), "v"(b[(v + 1) % kVar]));
+        asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+                     : "+a"(c3) : "v"(a[(v + 2) % kVar]), "v"(b[(v + 3) % kVar]));
+      }
+    }
+    // The last MFMAs' results are read by VALU code below: wait out their
+    // latency before the accumulators are read.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(c0), "+a"(c1), "+a"(c2), "+a"(c3));
+#pragma unroll
+    for (int j = 0; j < 16; j++) s += c0[j] + c1[j] + c2[j] + c3[j];
+  } else if (kShape == 3) {
+    f32x4 c[8] = {};
+    for (int i = 0; i < iters; i++) {
+#pragma unroll
+      for (int v = 0; v < kVar; v++)
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+          asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                       : "+a"(c[k]) : "v"(a[(v + k) % kVar]), "v"(b[(v + (k >> 1)) % kVar]));
+    }
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                 : "+a"(c[0]), "+a"(c[1]), "+a"(c[2]), "+a"(c[3]), "+a"(c[4]), "+a"(c[5]),
+                   "+a"(c[6]), "+a"(c[7]));
+#pragma unroll
+    for (int k = 0; k < 8; k++) s += c[k][0] + c[k][1] + c[k][2] + c[k][3];
   } else {
     // Twice the instructions of half the FLOPs each: eight f32x4 chains.
     f32x4 c[8] = {};
@@ -201,27 +237,29 @@ double h3probe_mfma_flops(int32_t blocks, int32_t iters) {
   return (double)blocks * (kThreads / 64) * iters * kVar * 4 * 32768.0;
 }
 
-// shape 0: v_mfma_f32_32x32x16_bf16, 1: v_mfma_f32_16x16x32_bf16. `ops` holds
+// shape 0: v_mfma_f32_32x32x16_bf16, 1: v_mfma_f32_16x16x32_bf16, with VGPR
+// accumulators; 2 and 3: the same shapes with AGPR accumulators. `ops` holds
 // h3probe_mfma_operand_bytes(blocks) bytes, `sink` blocks * 512 floats.
 // Returns 0, -1 on a bad argument, -2 on a launch failure.
 int h3probe_mfma(int32_t shape, const void* ops, int32_t blocks, int32_t iters, void* sink,
                  void* stream) {
-  if ((shape != 0 && shape != 1) || !ops || !sink || blocks <= 0 || iters <= 0) return -1;
+  if (shape < 0 || shape > 3 || !ops || !sink || blocks <= 0 || iters <= 0) return -1;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // 96 KiB of dynamic LDS keeps one workgroup per CU, as in the attention kernel.
   const int lds = 96 * 1024;
-  if (shape == 0) {
-    if (hipFuncSetAttribute((const void*)mfma_stream<0>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-      return -2;
-    mfma_stream<0><<<blocks, kThreads, lds, s>>>(static_cast<const bf16x8*>(ops), iters,
-                                                 static_cast<float*>(sink));
-  } else {
-    if (hipFuncSetAttribute((const void*)mfma_stream<1>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-      return -2;
-    mfma_stream<1><<<blocks, kThreads, lds, s>>>(static_cast<const bf16x8*>(ops), iters,
-                                                 static_cast<float*>(sink));
+  const void* fn = shape == 0   ? (const void*)mfma_stream<0>
+                   : shape == 1 ? (const void*)mfma_stream<1>
+                   : shape == 2 ? (const void*)mfma_stream<2>
+                                : (const void*)mfma_stream<3>;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+    return -2;
+  const bf16x8* o = static_cast<const bf16x8*>(ops);
+  float* sk = static_cast<float*>(sink);
+  switch (shape) {
+    case 0: mfma_stream<0><<<blocks, kThreads, lds, s>>>(o, iters, sk); break;
+    case 1: mfma_stream<1><<<blocks, kThreads, lds, s>>>(o, iters, sk); break;
+    case 2: mfma_stream<2><<<blocks, kThreads, lds, s>>>(o, iters, sk); break;
+    default: mfma_stream<3><<<blocks, kThreads, lds, s>>>(o, iters, sk); break;
   }
   return launch_status();
 }
