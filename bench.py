@@ -300,13 +300,17 @@ def mfma_ceiling_fns(dev, cus: int, iters: int = 2000):
             assert rc == 0, f"h3probe_mfma returned {rc}"
         return fn
     fns = {"mfma32_random": mk(0, rnd), "mfma32_zero": mk(0, zero),
-           "mfma16_random": mk(1, rnd)}
+           "mfma16_random": mk(1, rnd), "mfma32_agpr_acc_random": mk(2, rnd)}
     return fns, P.h3probe_mfma_flops(cus, iters), (rnd, zero, sink)
 
 
 RELAYOUT_VARIANTS = {0: "tokens-fastest 8x5x512", 1: "tokens-fastest 2x5x256",
                      2: "tokens-fastest 4x4x256", 3: "heads-fastest 4x4x256",
-                     4: "2x2 blocks 4x5x512"}
+                     4: "2x2 blocks 4x5x512", 8: "tokens-fastest 16x5x512",
+                     5: "tokens-fastest 8x5x512, default cache policy",
+                     6: "tokens-fastest 4x4x256, default cache policy",
+                     7: "tokens-fastest 16x5x512, default cache policy",
+                     9: "tokens-fastest 32x5x512, default cache policy"}
 
 
 def ceilings_extra(args, dev, cus: int, read_bytes: int, write_bytes: int, relayout=None):
