@@ -179,7 +179,9 @@ __global__ __launch_bounds__(256) void copy_stream(const u32x4* __restrict__ src
 // (contiguous reads); 2: a wave's four rows are 2 tokens x 2 heads. kTok
 // tokens per workgroup, kU rows in flight per thread; tokens >= rows are
 // written as zeros.
-template <int kTok, int kU, int kThr, int kMap>
+// kNt: non-temporal loads and stores (1) or the default cache policy (0),
+// which lets L2 gather the scattered head-major rows before they go out.
+template <int kTok, int kU, int kThr, int kMap, int kNt = 1>
 __global__ __launch_bounds__(kThr) void relayout_stream(const u32x4* __restrict__ in,
                                                        u32x4* __restrict__ out, int rows,
                                                        int rows_pad, int heads) {
@@ -205,8 +207,9 @@ __global__ __launch_bounds__(kThr) void relayout_stream(const u32x4* __restrict_
         hd[u] = 2 * (blk / (kTok / 2)) + (q >> 1);
       }
       const int s = s0 + tok[u];
+      const u32x4* src = in + ((int64_t)s * heads + hd[u]) * 16 + c;
       x[u] = (r < total && s < rows && hd[u] < heads)
-                 ? __builtin_nontemporal_load(in + ((int64_t)s * heads + hd[u]) * 16 + c)
+                 ? (kNt ? __builtin_nontemporal_load(src) : *src)
                  : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
@@ -214,7 +217,13 @@ __global__ __launch_bounds__(kThr) void relayout_stream(const u32x4* __restrict_
       const int r = p0 + u * kG + g;
       const int s = s0 + tok[u];
       if (r < total && s < rows_pad && hd[u] < heads)
-        __builtin_nontemporal_store(x[u], out + ((int64_t)hd[u] * rows_pad + s) * 16 + c);
+      {
+        u32x4* dst = out + ((int64_t)hd[u] * rows_pad + s) * 16 + c;
+        if (kNt)
+          __builtin_nontemporal_store(x[u], dst);
+        else
+          *dst = x[u];
+      }
     }
   }
 }
@@ -298,12 +307,14 @@ int h3probe_stream(int32_t kind, const void* src, void* dst, int64_t bytes, int3
 
 // The prologue's relayout without arithmetic: in [rows, heads * 128] bf16
 // token-major, out [heads, rows_pad, 128] head-major (rows_pad a multiple of
-// 8). variant: 0 tokens-fastest 8 tokens x 5 rows in flight x 512 threads,
+// 32). variant: 0 tokens-fastest 8 tokens x 5 rows in flight x 512 threads,
 // 1 tokens-fastest 2 x 5 x 256, 2 tokens-fastest 4 x 4 x 256, 3 heads-fastest
-// 4 x 4 x 256, 4 2x2 blocks 4 x 5 x 512.
+// 4 x 4 x 256, 4 2x2 blocks 4 x 5 x 512; with the default cache policy
+// instead of non-temporal: 5 tokens-fastest 8x5x512, 6 4x4x256, 7 16x5x512,
+// 9 32x5x512; 8 tokens-fastest 16x5x512 non-temporal.
 int h3probe_relayout(int32_t variant, const void* in, void* out, int32_t rows, int32_t rows_pad,
                      int32_t heads, void* stream) {
-  if (!in || !out || rows <= 0 || rows_pad < rows || rows_pad % 8 || heads <= 0 || heads % 2)
+  if (!in || !out || rows <= 0 || rows_pad < rows || rows_pad % 32 || heads <= 0 || heads % 2)
     return -1;
   if ((reinterpret_cast<uintptr_t>(in) & 15) || (reinterpret_cast<uintptr_t>(out) & 15)) return -1;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -315,6 +326,11 @@ int h3probe_relayout(int32_t variant, const void* in, void* out, int32_t rows, i
     case 2: relayout_stream<4, 4, 256, 0><<<rows_pad / 4, 256, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
     case 3: relayout_stream<4, 4, 256, 1><<<rows_pad / 4, 256, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
     case 4: relayout_stream<4, 5, 512, 2><<<rows_pad / 4, 512, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    case 5: relayout_stream<8, 5, 512, 0, 0><<<rows_pad / 8, 512, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    case 6: relayout_stream<4, 4, 256, 0, 0><<<rows_pad / 4, 256, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    case 7: relayout_stream<16, 5, 512, 0, 0><<<rows_pad / 16, 512, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    case 8: relayout_stream<16, 5, 512, 0, 1><<<rows_pad / 16, 512, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
+    case 9: relayout_stream<32, 5, 512, 0, 0><<<rows_pad / 32, 512, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
     default: return -1;
   }
   return launch_status();
