@@ -231,10 +231,6 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
   // sub-step's right after its last MFMA. B: the x operands, double-buffered
   // (buffer u for sub-step u).
   bf16x8 A[kNB], B[2][kMB];
-#pragma unroll
-  for (int nb = 0; nb < kNB; nb++) A[nb] = operand(lds, a_off[0], nb);
-#pragma unroll
-  for (int mb = 0; mb < kMB; mb++) B[0][mb] = operand(lds, b_off[0], mb);
 
   // MFMA k of a sub-step: block (nb, mb) = (k / kMB, k % kMB), W-major, so W
   // operand nb is free after MFMA kMB nb + kMB - 1.
@@ -248,6 +244,15 @@ __global__ __launch_bounds__(kPThreads, 1) void qkv_proj_kernel(ProjArgs a) {
     if (k < 2 * kMB && (k & 1) == 0) B[u2][k >> 1] = operand(stage, b_off[u2], k >> 1);
     if (k % kMB == kMB - 1) A[k / kMB] = operand(stage, a_off[u2], k / kMB);
   };
+  // Step 0's first-sub-step operands, read in the order the loop reads them:
+  // the compiler's LDS waits at the loop head then count the same reads on
+  // both entry paths. Read in any other order, its merged wait at the loop
+  // head is for every read before the first MFMA of each step.
+#pragma unroll
+  for (int k = 0; k < kMfmaSub; k++) {
+    reads_after(k, lds, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   for (int t = 0; t < steps; t++) {
     const uint16_t* cur_stage = lds + (t & 1) * kStageElems;

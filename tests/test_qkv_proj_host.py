@@ -13,6 +13,8 @@ no GPU.
   write (e.g. `v_readlane_b32` restoring a spilled SGPR) fewer than 5 wait
   states earlier catches a register allocation that would feed a load a stale
   offset.
+- Its main loop's first LDS wait: the compiler must wait only for the reads
+  the first MFMA needs, not for every read in flight.
 """
 import os
 import re
@@ -129,15 +131,36 @@ def test_dma_scan_finds_a_planted_hazard():
     assert _dma_hazards(good) == (1, 0)
 
 
-def test_qkv_proj_dma_loads_hazard_free(tmp_path):
+@pytest.fixture(scope="module")
+def qkv_asm(tmp_path_factory):
+    """gfx950 assembly of csrc/qkv_proj.hip."""
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(hipcc):
         pytest.skip("hipcc not found")
-    out = tmp_path / "qkv_proj.s"
+    out = tmp_path_factory.mktemp("asm") / "qkv_proj.s"
     subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
                     "-Xclang", "-packed-fp32-ops", f"-I{CSRC}", f"-I{os.path.join(ROOT, 'include')}",
                     "--cuda-device-only", "-S", "-o", str(out), os.path.join(CSRC, "qkv_proj.hip")],
                    check=True, capture_output=True)
-    loads, hazards = _dma_hazards(out.read_text())
+    return out.read_text()
+
+
+def test_qkv_proj_dma_loads_hazard_free(qkv_asm):
+    loads, hazards = _dma_hazards(qkv_asm)
     assert loads > 0
     assert hazards == 0, f"{hazards} of {loads} LDS-DMA loads read an SGPR a VALU op wrote < 5 wait states earlier"
+
+
+def test_main_loop_head_waits_only_for_its_operands(qkv_asm):
+    """The first MFMA of each reduction step needs two operand reads issued
+    early in the previous step; ten reads issued after them may still be in
+    flight. A wait for (nearly) all reads at the loop head -- what the
+    compiler emits when the reads before the loop come in another order than
+    the loop's -- idles the matrix cores at every step."""
+    lines = qkv_asm.splitlines()
+    heads = [i for i, ln in enumerate(lines) if "Inner Loop Header" in ln]
+    assert len(heads) == 6   # one main loop per kernel instantiation
+    for i in heads:
+        wait = next(re.search(r"lgkmcnt\((\d+)\)", ln) for ln in lines[i:i + 20]
+                    if "s_waitcnt" in ln and "lgkmcnt" in ln)
+        assert int(wait.group(1)) >= 8, lines[i:i + 12]
