@@ -231,6 +231,28 @@ def profile_only(args, env) -> int:
         torch.cuda.synchronize()
         print(f"qkv: {args.steps} launches, x [{S}, {C_HIDDEN}] x W^T -> Q, K, V [{H}, {S_pad}, {D}]")
         return 0
+    if args.only == "gemms":
+        # This library's plain and fused QKV projections, hipBLASLt's QKV GEMM
+        # (torch.mm), this library's and hipBLASLt's out-projection, in turn.
+        x, w = qkv_inputs(env)
+        w_out = (torch.randn((C_HIDDEN, H * D), generator=env["g"], device=dev) * 0.02).to(torch.bfloat16)
+        vh = torch.empty_like(env["qh"])
+        qkv = torch.empty((S, 3 * H * D), dtype=torch.bfloat16, device=dev)
+        y = torch.empty((S, C_HIDDEN), dtype=torch.bfloat16, device=dev)
+        att = x[:, :H * D]
+        table = ops.rope_table(env["pos"], env["ax"], env["inv"])
+        out = (env["qh"], env["kh"], vh)
+        for _ in range(args.warmup + args.steps):
+            ops.qkv_proj(x, w, heads=H, seq_pad=S_pad, out=out)
+            torch.mm(x, w.t(), out=qkv)
+            ops.qkv_proj(x, w, env["gq"], env["gk"], table, heads=H, eps=env["C"].QK_EPS,
+                         seq_pad=S_pad, out=out)
+            ops.out_proj(att, w_out, out=y)
+            torch.mm(att, w_out.t(), out=y)
+        torch.cuda.synchronize()
+        print(f"gemms: {args.steps} rounds of plain QKV, hipBLASLt QKV, fused QKV, out-projection, "
+              f"hipBLASLt out-projection at config 3")
+        return 0
     if args.only == "attention":
         env["prologue"]()
         for _ in range(args.warmup + args.steps):
@@ -611,11 +633,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--only", choices=("attention", "prologue", "copy", "qkv", "anchor",
+    ap.add_argument("--only", choices=("attention", "prologue", "copy", "qkv", "gemms", "anchor",
                                        "mfma_ceiling"),
                     help="profiling mode: run one kernel --steps times at config 3 (prologue: "
                          "config 5, Q and K only; copy: a plain 1 GiB device copy for counter "
-                         "calibration; qkv: the fused QKV projection; anchor: this library's "
+                         "calibration; qkv: the fused QKV projection; gemms: the projections and "
+                         "hipBLASLt's GEMMs of the same shapes in turn; anchor: this library's "
                          "attention and torch's flash SDPA alternately, dense, at config 4's "
                          "padded shape; mfma_ceiling: the sustained 32x32x16 MFMA stream) and "
                          "print nothing but a one-line summary")
