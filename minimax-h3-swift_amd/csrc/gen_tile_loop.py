@@ -365,19 +365,26 @@ def rescale_code(em, label, sb):
     em.emit("s_nop 2", f"s_branch {label}_rescaled")
 
 
+def column_load():
+    """col[j + 3] (clamped to n - 1; ST1 holds n - 1) for the K load two blocks
+    on, issued at the start of a FIRST/FULL block so that its latency passes
+    under the block's MFMAs; the block-end lgkmcnt(0) collects it. An SMEM
+    load may complete out of order with the LDS reads, so with it in flight
+    lgkmcnt(N) still means "the reads before the last N are done" (it may
+    also wait for the load): the block's counted waits stay exact for LDS."""
+    return [f"s_add_u32 {SIDX}, {SJ}, 3",
+            f"s_min_u32 {SIDX}, {SIDX}, {ST1}",
+            f"s_lshl_b32 {SIDX}, {SIDX}, 2",
+            f"s_load_dword {SCOL}, {COLP}, {SIDX}"]
+
+
 def block_end(em, kind, p, label, sb):
-    """Rescale (FULL/LAST), next column load (FIRST/FULL), waits, ragged V
-    zeroing (LAST/ONLY), barrier, column shift."""
+    """Rescale (FULL/LAST), waits (which also collect the column load of
+    FIRST/FULL blocks), ragged V zeroing (LAST/ONLY), barrier, column shift."""
     if kind in ("FULL", "LAST"):
         em.emit(f"s_cmp_lg_u64 {RAISE}, 0",
                 f"s_cbranch_scc1 {label}_rescale",
                 f"{label}_rescaled:")
-    if kind in ("FIRST", "FULL"):
-        # col[j + 3] (clamped to n - 1) for the next iteration's K load.
-        em.emit(f"s_add_u32 {SIDX}, {SJ}, 3",
-                f"s_min_u32 {SIDX}, {SIDX}, {ST1}",
-                f"s_lshl_b32 {SIDX}, {SIDX}, 2",
-                f"s_load_dword {SCOL}, {COLP}, {SIDX}")
     em.emit("s_waitcnt vmcnt(0) lgkmcnt(0)")
     if kind in ("LAST", "ONLY"):
         # Rows >= seq_len of V(j) are zeroed after they land (0 * NaN is NaN):
@@ -446,6 +453,8 @@ def gen_block(em, kind, p, label, out_of_line):
         kd = dma_lines("k", p)
     pre += rsrc_setup("v", SC0, "%[vb_lo]", "%[vb_hi]", "%[vrec]", "%[vstep]")
     pre += [f"s_sub_u32 {ST1}, %[n], 1"]      # n - 1, the column-load clamp
+    if has_s:
+        pre += column_load()
     vd = dma_lines("v", p)
     dmas = []
     for i in range(max(len(kd), len(vd))):

@@ -181,3 +181,17 @@ def test_every_ring_mfma_waits_for_its_reads(gen, lines):
                 src_a = _regs(parts[1]) & ring
                 for p in pending:
                     assert not (p & src_a), f"{ln} reads a ring entry still being loaded"
+
+
+def test_column_load_early_and_collected(gen, lines):
+    """The next column index (s_load into SCOL) is issued at the start of its
+    block, with the block's MFMAs between it and the lgkmcnt(0) that collects
+    it, and nothing reads SCOL before that wait."""
+    loads = [i for i, ln in enumerate(lines) if ln.startswith("s_load_dword")]
+    assert loads
+    for i in loads:
+        assert lines[i].split()[1].rstrip(",") == gen.SCOL
+        j = next(k for k in range(i + 1, len(lines)) if "lgkmcnt(0)" in lines[k])
+        between = lines[i + 1:j]
+        assert sum(ln.startswith("v_mfma") for ln in between) >= 8, lines[i]
+        assert not any(gen.SCOL in ln for ln in between), lines[i]
