@@ -38,9 +38,9 @@
 // weight times a zeroed V row is NaN.)
 // The rescale is lazy: m is only raised when a tile's max exceeds it by more
 // than 2^8, which keeps every exponentiated score <= 256 and changes nothing
-// in exact arithmetic (numerator and denominator share m). l sums the bf16-rounded
-// weights that O accumulates, so both sides of the quotient see the same
-// weights. The output is O / max(l, 1e-30).
+// in exact arithmetic (numerator and denominator share m). l sums the fp32
+// weights, as the reference's recurrence does; O accumulates their bf16
+// roundings, the P operand of the P V product. The output is O / max(l, 1e-30).
 #include <cmath>
 
 #include "common.h"

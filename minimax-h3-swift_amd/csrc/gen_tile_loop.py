@@ -10,7 +10,7 @@ tile. Per tile j each wave issues, in one instruction stream,
 
   * the scores of the next tile, S(j+1) = K(j+1) Q^T (16 MFMAs),
   * the product of the previous one, O += V(j-1)^T P(j-1) (16 MFMAs),
-  * the online softmax of S(j) into P(j) (about 130 VALU instructions),
+  * the online softmax of S(j) into P(j) (about 145 VALU instructions),
   * its share of the HBM -> LDS loads of K(j+2) and V(j) (8 buffer loads),
 
 so its VALU work runs beside its own MFMAs, and the partner wave on the
@@ -99,7 +99,6 @@ DK0 = 114       # K load lane offsets: v[114 + i], i < LOADS
 DV0 = DK0 + LOADS  # V load lane offsets
 MX, SW, AL, LA, LB = 122, 123, 124, 125, 126
 N_VGPR = 127
-BF16_ONES = "0x3f803f80"   # (1.0, 1.0) as packed bf16
 KEYOFF = 120    # a120: kh*64 + 4hh            (input)
 LANE16 = 121    # a121: 16 * lane              (input)
 ROWB = 122      # a122: ROWS_PER_WAVE*w + lane/16  (input)
@@ -196,10 +195,13 @@ def softmax_ops(sb, pb):
     ops.append(f"v_sub_f32 v{AL}, v{M}, v{SW}")
     ops.append(f"v_mov_b32 v{M}, v{SW}")
     ops.append(f"v_exp_f32 v{AL}, v{AL}")
-    # Weights 2^(s*c - m) in batches of four, packed to bf16 P and summed as
-    # bf16 (the weights P V uses). The pack of batch b-1 and the sum of batch
-    # b-2 follow batch b's exponentials, a batch behind their producers.
-    cvt_prev, dot_prev2, dot_prev = [], [], []
+    # Weights 2^(s*c - m) in batches of four, packed to bf16 P and summed in
+    # fp32 into l (two chains). The pack and the sums of batch b-1 follow
+    # batch b's exponentials, a batch behind their producers. The sums are
+    # plain VALU adds: v_dot2c over the packed weights would run on the
+    # matrix pipeline, and there each one costs the MFMAs about as many
+    # cycles as half a 32x32x16 product.
+    prev = []
     for b in range(8):
         idx = list(range(4 * b, 4 * b + 4))
         for i in idx:
@@ -208,26 +210,18 @@ def softmax_ops(sb, pb):
             ops.append(f"v_mul_f32 v{L}, v{L}, v{AL}")
         for i in idx:
             ops.append(f"v_exp_f32 v{x[i]}, v{x[i]}")
-        ops.extend(cvt_prev)
-        ops.extend(dot_prev2)
-        dot_prev2 = dot_prev
-        cvt_prev, dot_prev = [], []
+        ops.extend(prev)
+        prev = []
         # score i (= 16kb + r) -> P chunk kc = 2kb + (r >= 8), element r & 7
         for pair in range(2):
             i0 = 4 * b + 2 * pair
             kb, r = i0 // 16, i0 % 16
             kc = 2 * kb + (r >> 3)
             e = (r & 7) >> 1
-            dst = p_reg(pb, kc, e)
-            cvt_prev.append(f"v_cvt_pk_bf16_f32 v{dst}, v{x[i0]}, v{x[i0 + 1]}")
-            acc = LA if (e & 1) == 0 else LB
-            dot_prev.append(f"v_dot2c_f32_bf16 v{acc}, {BF16_ONES}, v{dst}")
-    ops.extend(cvt_prev)
-    ops.extend(dot_prev2)
-    ops.extend(dot_prev)
-    # v_dot2c runs on the matrix pipeline: a plain VALU read of its result
-    # needs wait states the hardware does not enforce.
-    ops.append("s_nop 4")
+            prev.append(f"v_cvt_pk_bf16_f32 v{p_reg(pb, kc, e)}, v{x[i0]}, v{x[i0 + 1]}")
+            prev.append(f"v_add_f32 v{LA}, v{LA}, v{x[i0]}")
+            prev.append(f"v_add_f32 v{LB}, v{LB}, v{x[i0 + 1]}")
+    ops.extend(prev)
     ops.append(f"v_add_f32 v{LA}, v{LA}, v{LB}")
     ops.append(f"v_add_f32 v{L}, v{L}, v{LA}")
     return ops

@@ -4,9 +4,6 @@ These CPU tests check that the committed include is what the generator
 writes, and scan the generated instruction stream for the hazards the
 hardware does not interlock and the generator must space out itself:
 
-- a v_dot2c result read by a plain VALU instruction (dot runs on the matrix
-  pipeline; a read within 4 wait states sees the old value -- this produced a
-  per-row scale error in l before the gap existed);
 - a v_exp_f32 result consumed by the next instruction;
 - a VGPR written by VALU and read by v_permlane32_swap within 2 wait states;
 - M0 written and used by an LDS DMA load in the next instruction;
@@ -15,7 +12,11 @@ hardware does not interlock and the generator must space out itself:
 - an MFMA result read by a VALU instruction fewer than 12 wait states later
   within straight-line code;
 - ds_read waits: every MFMA reading a ring entry is preceded by an
-  s_waitcnt lgkmcnt(N) that leaves only later reads outstanding.
+  s_waitcnt lgkmcnt(N) that leaves only later reads outstanding;
+
+and that the softmax adds every exponentiated score of a tile into the row
+sum exactly once, after its exponential. Each scan is also run on a copy of
+the stream with one such mistake planted, and must find it.
 """
 import importlib.util
 import os
@@ -88,8 +89,6 @@ def _reads_within(seg, i, dst, states, reader):
         op, parts = _split(ln)
         if reader(op) and len(parts) > 1 and _regs(",".join(parts[1:])) & dst:
             return True
-        if reader(op) and op.startswith("v_dot2c") and _regs(parts[0]) & dst:
-            return True
         gap += _wait_states(ln)
     return False
 
@@ -107,24 +106,19 @@ def test_register_budget(gen, lines):
     assert vmax < 128 and amax < 128, (vmax, amax)
 
 
-def test_dot_results_not_read_early(lines):
-    for seg in _straight_segments(lines):
-        for i, ln in enumerate(seg):
-            if ln.startswith("v_dot2c"):
-                dst = _regs(_split(ln)[1][0])
-                plain = lambda op: op.startswith("v_") and not op.startswith("v_dot2c")
-                assert not _reads_within(seg, i, dst, 5, plain), ln
-
-
-def test_exp_results_not_read_next(lines):
+def exp_read_next(lines):
+    bad = []
     for seg in _straight_segments(lines):
         for i, ln in enumerate(seg):
             if ln.startswith("v_exp_f32"):
                 dst = _regs(_split(ln)[1][0])
-                assert not _reads_within(seg, i, dst, 2, lambda op: op.startswith("v_")), ln
+                if _reads_within(seg, i, dst, 2, lambda op: op.startswith("v_")):
+                    bad.append(ln)
+    return bad
 
 
-def test_permlane_sources_settled(lines):
+def permlane_unsettled(lines):
+    bad = []
     for seg in _straight_segments(lines):
         for i, ln in enumerate(seg):
             op, parts = _split(ln)
@@ -132,38 +126,39 @@ def test_permlane_sources_settled(lines):
                 dst = _regs(parts[0])
                 if not dst or any(k == "a" for k, _ in dst):
                     continue
-                assert not _reads_within(seg, i, dst, 2,
-                                         lambda o: o.startswith("v_permlane")), ln
+                if _reads_within(seg, i, dst, 2, lambda o: o.startswith("v_permlane")):
+                    bad.append(ln)
+    return bad
 
 
-def test_m0_settled_before_lds_dma(lines):
-    for a, b in zip(lines, lines[1:]):
-        if a.startswith("s_add_u32 m0") or a.startswith("s_mov_b32 m0"):
-            assert not (b.startswith("buffer_load") and b.endswith("lds")), (a, b)
+def m0_unsettled(lines):
+    return [(a, b) for a, b in zip(lines, lines[1:])
+            if (a.startswith("s_add_u32 m0") or a.startswith("s_mov_b32 m0"))
+            and b.startswith("buffer_load") and b.endswith("lds")]
 
 
-def test_ring_entry_not_overwritten_right_after_its_mfma(gen, lines):
+def ring_overwritten(gen, lines):
     ring = {("a", i) for i in range(gen.RING, gen.RING + 4 * gen.RING_N)}
-    for a, b in zip(lines, lines[1:]):
-        if a.startswith("v_mfma") and b.startswith("ds_read"):
-            src_a = _regs(_split(a)[1][1]) & ring
-            dst = _regs(_split(b)[1][0])
-            assert not (src_a & dst), (a, b)
+    return [(a, b) for a, b in zip(lines, lines[1:])
+            if a.startswith("v_mfma") and b.startswith("ds_read")
+            and _regs(_split(a)[1][1]) & ring & _regs(_split(b)[1][0])]
 
 
-def test_mfma_results_not_read_by_valu_soon(lines):
+def mfma_read_soon(lines):
+    bad = []
+    valu = lambda op: op.startswith("v_") and not op.startswith("v_mfma")
     for seg in _straight_segments(lines):
         for i, ln in enumerate(seg):
-            if ln.startswith("v_mfma"):
-                dst = _regs(_split(ln)[1][0])
-                valu = lambda op: op.startswith("v_") and not op.startswith("v_mfma")
-                assert not _reads_within(seg, i, dst, 12, valu), ln
+            if ln.startswith("v_mfma") and _reads_within(seg, i, _regs(_split(ln)[1][0]), 12, valu):
+                bad.append(ln)
+    return bad
 
 
-def test_every_ring_mfma_waits_for_its_reads(gen, lines):
+def ring_unwaited(gen, lines):
     """Replays lgkmcnt: each ds_read into the ring is outstanding until a wait
     leaves fewer reads pending than were issued after it."""
     ring = {("a", i) for i in range(gen.RING, gen.RING + 4 * gen.RING_N)}
+    bad = []
     for seg in _straight_segments(lines):
         pending = []  # register sets of outstanding ring reads, oldest first
         for ln in seg:
@@ -179,8 +174,92 @@ def test_every_ring_mfma_waits_for_its_reads(gen, lines):
                     pending = pending[len(pending) - keep:] if keep else []
             elif op.startswith("v_mfma"):
                 src_a = _regs(parts[1]) & ring
-                for p in pending:
-                    assert not (p & src_a), f"{ln} reads a ring entry still being loaded"
+                if any(p & src_a for p in pending):
+                    bad.append(ln)
+    return bad
+
+
+def row_sum_gaps(gen, ops, sb):
+    """Scores of S(sb) not added into the row-sum chains (LA, LB) exactly once
+    after their exponential."""
+    chains = {("v", gen.LA), ("v", gen.LB)}
+    x = {("v", gen.s_reg(sb, i)) for i in range(32)}
+    done, added, bad = set(), {}, []
+    for ln in ops:
+        op, parts = _split(ln)
+        if op == "v_exp_f32":
+            done |= _regs(parts[0]) & x
+        elif op == "v_add_f32" and _regs(parts[0]) & chains:
+            for r in _regs(",".join(parts[1:])) & x:
+                if r not in done:
+                    bad.append(ln)
+                added[r] = added.get(r, 0) + 1
+    return bad + [r for r in sorted(x) if added.get(r, 0) != 1]
+
+
+def _plant_after(lines, pred, extra):
+    i = next(k for k, ln in enumerate(lines) if pred(ln))
+    return lines[:i + 1] + [extra(lines[i])] + lines[i + 1:]
+
+
+def test_exp_results_not_read_next(lines):
+    assert exp_read_next(lines) == []
+    dst = lambda ln: _split(ln)[1][0]
+    planted = _plant_after(lines, lambda ln: ln.startswith("v_exp_f32"),
+                           lambda ln: f"v_add_f32 v122, v122, {dst(ln)}")
+    assert exp_read_next(planted)
+
+
+def test_permlane_sources_settled(lines):
+    assert permlane_unsettled(lines) == []
+    i = next(k for k, ln in enumerate(lines) if ln.startswith("v_permlane"))
+    src = _split(lines[i])[1][1]
+    assert permlane_unsettled(lines[:i] + [f"v_mov_b32 {src}, v96"] + lines[i:])
+
+
+def test_m0_settled_before_lds_dma(lines):
+    assert m0_unsettled(lines) == []
+    i = next(k for k, ln in enumerate(lines) if ln.startswith("buffer_load") and ln.endswith("lds"))
+    assert lines[i - 1].startswith("s_nop")
+    assert m0_unsettled(lines[:i - 1] + lines[i:])
+
+
+def test_ring_entry_not_overwritten_right_after_its_mfma(gen, lines):
+    assert ring_overwritten(gen, lines) == []
+    src_a = lambda ln: _split(ln)[1][1]
+    planted = _plant_after(lines, lambda ln: ln.startswith("v_mfma") and "a[9" in src_a(ln),
+                           lambda ln: f"ds_read_b128 {src_a(ln)}, v98")
+    assert ring_overwritten(gen, planted)
+
+
+def test_mfma_results_not_read_by_valu_soon(lines):
+    assert mfma_read_soon(lines) == []
+    dst = lambda ln: _split(ln)[1][0]
+    planted = _plant_after(lines, lambda ln: ln.startswith("v_mfma") and dst(ln).startswith("v["),
+                           lambda ln: f"v_max_f32 v122, v122, v{dst(ln)[2:].split(':')[0]}")
+    assert mfma_read_soon(planted)
+
+
+def test_every_ring_mfma_waits_for_its_reads(gen, lines):
+    assert ring_unwaited(gen, lines) == []
+    # Loosen the first wait that leaves reads outstanding before a ring MFMA.
+    i = next(k for k, ln in enumerate(lines)
+             if re.fullmatch(r"s_waitcnt lgkmcnt\([1-9]\d*\)", ln) and lines[k + 1].startswith("v_mfma"))
+    n = int(re.search(r"\((\d+)\)", lines[i]).group(1))
+    planted = lines[:i] + [f"s_waitcnt lgkmcnt({n + 1})"] + lines[i + 1:]
+    assert ring_unwaited(gen, planted)
+
+
+def test_row_sum_adds_every_weight_once(gen):
+    for sb, pb in ((0, 0), (1, 1), (0, 1), (1, 0)):
+        ops = gen.softmax_ops(sb, pb)
+        assert row_sum_gaps(gen, ops, sb) == []
+    ops = gen.softmax_ops(0, 0)
+    i = next(k for k, ln in enumerate(ops) if ln.startswith(f"v_add_f32 v{gen.LB}, v{gen.LB}, v"))
+    assert row_sum_gaps(gen, ops[:i] + ops[i + 1:], 0)          # a weight left out
+    j = next(k for k, ln in enumerate(ops) if ln.startswith("v_exp_f32 v0,"))
+    early = f"v_add_f32 v{gen.LA}, v{gen.LA}, {_split(ops[j])[1][0]}"
+    assert row_sum_gaps(gen, ops[:j] + [early] + ops[j:], 0)   # added before its exponential
 
 
 def test_column_load_early_and_collected(gen, lines):
