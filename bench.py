@@ -221,6 +221,12 @@ def profile_only(args, env) -> int:
         torch.cuda.synchronize()
         print(f"mfma_ceiling: {args.steps} launches of the 32x32x16 stream on random operands")
         return 0
+    if args.only == "issue":
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        res = issue_probe(dev, cus)
+        print("issue: " + "; ".join(f"{k} ({v['what']}) {v['cycles_per_iter']} cycles, "
+                                     f"MFMA busy {v['mfma_busy']}" for k, v in res.items()))
+        return 0
     if args.only == "qkv":
         x, w = qkv_inputs(env)
         vh = torch.empty_like(env["qh"])
@@ -288,6 +294,9 @@ def probe_lib():
     L.h3probe_stream.argtypes = [i32, vp, vp, i64, i32, i32, vp, vp]
     L.h3probe_relayout.restype = ctypes.c_int
     L.h3probe_relayout.argtypes = [i32, vp, vp, i32, i32, i32, vp]
+    L.h3probe_issue_operand_bytes.restype, L.h3probe_issue_operand_bytes.argtypes = i64, [i32]
+    L.h3probe_issue.restype = ctypes.c_int
+    L.h3probe_issue.argtypes = [i32, vp, i32, i32, vp, vp]
     return L
 
 
@@ -326,6 +335,40 @@ def mfma_ceiling_fns(dev, cus: int, iters: int = 2000):
     return fns, P.h3probe_mfma_flops(cus, iters), (rnd, zero, sink)
 
 
+ISSUE_MIXES = {0: "4 mfma32", 1: "4 mfma32 + 4 x (fma, max3, exp)",
+               2: "mix 1 + 2 v_dot2c_f32_bf16", 3: "mix 1 + 4 v_add_f32",
+               4: "mix 1 + 1 v_mfma_f32_4x4x4bf16_1k"}
+
+
+def issue_probe(dev, cus: int, iters: int = 4000) -> dict:
+    """Shader-clock cycles per iteration of each issue mix (probes/ceilings.hip,
+    issue_mix: four v_mfma_f32_32x32x16_bf16 with the mix's instructions after
+    them, 8 waves per CU on random operands). Per workgroup the slowest of its
+    waves gives the iteration time of a SIMD running two of them; the median
+    over workgroups is reported, with the matrix cores' busy fraction
+    (8 MFMAs x 32 cycles per iteration per SIMD)."""
+    import numpy as np
+    import torch
+    P = probe_lib()
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
+    ops = torch.randn(P.h3probe_issue_operand_bytes(cus) // 2, generator=g,
+                      device=dev).to(torch.bfloat16)
+    cyc = torch.zeros(cus * 8, dtype=torch.int64, device=dev)
+    out = {}
+    for mix, label in ISSUE_MIXES.items():
+        for _ in range(2):   # the first launch warms up
+            rc = P.h3probe_issue(mix, ctypes_ptr(ops.data_ptr()), cus, iters,
+                                 ctypes_ptr(cyc.data_ptr()), _stream_ptr())
+            assert rc == 0, f"h3probe_issue returned {rc}"
+        torch.cuda.synchronize()
+        per_wg = cyc.view(cus, 8).max(dim=1).values.cpu().numpy() / iters
+        c = float(np.median(per_wg))
+        out[f"mix{mix}"] = {"what": label, "cycles_per_iter": round(c, 1),
+                            "mfma_busy": round(8 * 32 / c, 4)}
+    return out
+
+
 RELAYOUT_VARIANTS = {0: "tokens-fastest 8x5x512", 1: "tokens-fastest 2x5x256",
                      2: "tokens-fastest 4x4x256", 3: "heads-fastest 4x4x256",
                      4: "2x2 blocks 4x5x512", 8: "tokens-fastest 16x5x512",
@@ -352,6 +395,7 @@ def ceilings_extra(args, dev, cus: int, read_bytes: int, write_bytes: int, relay
         res[name + "_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
         res[name + "_peak_frac"] = round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
     del keep
+    res["issue_probe"] = issue_probe(dev, cus)
     P = probe_lib()
     nbytes = max(read_bytes, write_bytes)
     src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
@@ -634,14 +678,15 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--only", choices=("attention", "prologue", "copy", "qkv", "gemms", "anchor",
-                                       "mfma_ceiling"),
+                                       "mfma_ceiling", "issue"),
                     help="profiling mode: run one kernel --steps times at config 3 (prologue: "
                          "config 5, Q and K only; copy: a plain 1 GiB device copy for counter "
                          "calibration; qkv: the fused QKV projection; gemms: the projections and "
                          "hipBLASLt's GEMMs of the same shapes in turn; anchor: this library's "
                          "attention and torch's flash SDPA alternately, dense, at config 4's "
-                         "padded shape; mfma_ceiling: the sustained 32x32x16 MFMA stream) and "
-                         "print nothing but a one-line summary")
+                         "padded shape; mfma_ceiling: the sustained 32x32x16 MFMA stream; "
+                         "issue: the MFMA/VALU issue-mix probe, printed per mix) and print "
+                         "nothing but a one-line summary")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -10,6 +10,10 @@
 //    bench.py can sweep them and keep the best.
 //  * h3probe_relayout: the prologue's token-major -> head-major layout change
 //    without arithmetic, in several thread mappings.
+//  * h3probe_issue: cycles per iteration (the shader clock, s_memtime) of an
+//    MFMA stream with softmax-like VALU work between its MFMAs, two waves per
+//    SIMD: how much of each kind of instruction the matrix cores absorb. The
+//    attention kernel's row sum chose v_add_f32 over v_dot2c from it.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -232,6 +236,104 @@ int launch_status() {
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
+// Issue mixes. One iteration: four independent v_mfma_f32_32x32x16_bf16
+// (operands v[0:15], accumulators a[0:63]), each followed by the mix's
+// instructions. The VALU work reads v[0:15] and writes v[16:49], which
+// nothing reads back within the loop, so the mixes differ only in what they
+// issue:
+//   0  MFMAs alone;
+//   1  + per MFMA v_fma_f32, v_max3_f32, v_exp_f32 (the softmax's shape:
+//      about 3.5 non-sum VALU instructions per MFMA in the attention loop);
+//   2  mix 1 + a v_dot2c_f32_bf16 after every second MFMA (the row sum over
+//      packed bf16 weights: 16 per 32 MFMAs);
+//   3  mix 1 + a v_add_f32 after every MFMA (the row sum over fp32 weights:
+//      32 per 32 MFMAs);
+//   4  mix 1 + one v_mfma_f32_4x4x4bf16_1k per four MFMAs (a row sum on the
+//      matrix cores: 8 per 32 MFMAs).
+#define H3P_MF0 "v_mfma_f32_32x32x16_bf16 a[0:15], v[0:3], v[4:7], a[0:15]\n"
+#define H3P_MF1 "v_mfma_f32_32x32x16_bf16 a[16:31], v[8:11], v[12:15], a[16:31]\n"
+#define H3P_MF2 "v_mfma_f32_32x32x16_bf16 a[32:47], v[0:3], v[12:15], a[32:47]\n"
+#define H3P_MF3 "v_mfma_f32_32x32x16_bf16 a[48:63], v[8:11], v[4:7], a[48:63]\n"
+#define H3P_SMX(a, b, c) \
+  "v_fma_f32 v" #a ", v1, v2, v3\n v_max3_f32 v" #b ", v4, v5, v6\n v_exp_f32 v" #c ", v7\n"
+#define H3P_SM0 H3P_SMX(16, 17, 18)
+#define H3P_SM1 H3P_SMX(19, 20, 21)
+#define H3P_SM2 H3P_SMX(22, 23, 24)
+#define H3P_SM3 H3P_SMX(25, 26, 27)
+#define H3P_DOT(d) "v_dot2c_f32_bf16 v" #d ", v8, v9\n"
+#define H3P_ADD(d) "v_add_f32 v" #d ", v10, v11\n"
+#define H3P_M4 "v_mfma_f32_4x4x4bf16_1k a[64:67], v[12:13], v[14:15], a[64:67]\n"
+#define H3P_CLOBBERS                                                                          \
+  "v16", "v17", "v18", "v19", "v20", "v21", "v22", "v23", "v24", "v25", "v26", "v27", "v28",  \
+      "v29", "v30", "v31", "v32", "v33", "a0", "a1", "a2", "a3", "a4", "a5", "a6", "a7", "a8",  \
+      "a9", "a10", "a11", "a12", "a13", "a14", "a15", "a16", "a17", "a18", "a19", "a20", "a21", \
+      "a22", "a23", "a24", "a25", "a26", "a27", "a28", "a29", "a30", "a31", "a32", "a33", "a34", \
+      "a35", "a36", "a37", "a38", "a39", "a40", "a41", "a42", "a43", "a44", "a45", "a46", "a47", \
+      "a48", "a49", "a50", "a51", "a52", "a53", "a54", "a55", "a56", "a57", "a58", "a59", "a60", \
+      "a61", "a62", "a63", "a64", "a65", "a66", "a67"
+
+template <int kMix>
+__global__ __launch_bounds__(kThreads, 1) void issue_mix(const u32x4* __restrict__ ops,
+                                                         int iters,
+                                                         unsigned long long* __restrict__ cycles) {
+  const int gid = blockIdx.x * kThreads + threadIdx.x;
+  const u32x4 x0 = ops[4 * gid], x1 = ops[4 * gid + 1], x2 = ops[4 * gid + 2],
+              x3 = ops[4 * gid + 3];
+  // Random operands into v[0:15], accumulators cleared.
+  asm volatile(
+      "v_mov_b32 v0, %0\n v_mov_b32 v1, %1\n v_mov_b32 v2, %2\n v_mov_b32 v3, %3\n"
+      "v_mov_b32 v4, %4\n v_mov_b32 v5, %5\n v_mov_b32 v6, %6\n v_mov_b32 v7, %7\n"
+      "v_mov_b32 v8, %8\n v_mov_b32 v9, %9\n v_mov_b32 v10, %10\n v_mov_b32 v11, %11\n"
+      "v_mov_b32 v12, %12\n v_mov_b32 v13, %13\n v_mov_b32 v14, %14\n v_mov_b32 v15, %15"
+      :
+      : "v"(x0[0]), "v"(x0[1]), "v"(x0[2]), "v"(x0[3]), "v"(x1[0]), "v"(x1[1]), "v"(x1[2]),
+        "v"(x1[3]), "v"(x2[0]), "v"(x2[1]), "v"(x2[2]), "v"(x2[3]), "v"(x3[0]), "v"(x3[1]),
+        "v"(x3[2]), "v"(x3[3])
+      : "v0", "v1", "v2", "v3", "v4", "v5", "v6", "v7", "v8", "v9", "v10", "v11", "v12", "v13",
+        "v14", "v15");
+  asm volatile(
+      "v_accvgpr_write_b32 a0, 0\n v_accvgpr_write_b32 a1, 0\n v_accvgpr_write_b32 a2, 0\n v_accvgpr_write_b32 a3, 0\n"
+      "v_accvgpr_write_b32 a4, 0\n v_accvgpr_write_b32 a5, 0\n v_accvgpr_write_b32 a6, 0\n v_accvgpr_write_b32 a7, 0\n"
+      "v_accvgpr_write_b32 a8, 0\n v_accvgpr_write_b32 a9, 0\n v_accvgpr_write_b32 a10, 0\n v_accvgpr_write_b32 a11, 0\n"
+      "v_accvgpr_write_b32 a12, 0\n v_accvgpr_write_b32 a13, 0\n v_accvgpr_write_b32 a14, 0\n v_accvgpr_write_b32 a15, 0\n"
+      "v_accvgpr_write_b32 a16, 0\n v_accvgpr_write_b32 a17, 0\n v_accvgpr_write_b32 a18, 0\n v_accvgpr_write_b32 a19, 0\n"
+      "v_accvgpr_write_b32 a20, 0\n v_accvgpr_write_b32 a21, 0\n v_accvgpr_write_b32 a22, 0\n v_accvgpr_write_b32 a23, 0\n"
+      "v_accvgpr_write_b32 a24, 0\n v_accvgpr_write_b32 a25, 0\n v_accvgpr_write_b32 a26, 0\n v_accvgpr_write_b32 a27, 0\n"
+      "v_accvgpr_write_b32 a28, 0\n v_accvgpr_write_b32 a29, 0\n v_accvgpr_write_b32 a30, 0\n v_accvgpr_write_b32 a31, 0\n"
+      "v_accvgpr_write_b32 a32, 0\n v_accvgpr_write_b32 a33, 0\n v_accvgpr_write_b32 a34, 0\n v_accvgpr_write_b32 a35, 0\n"
+      "v_accvgpr_write_b32 a36, 0\n v_accvgpr_write_b32 a37, 0\n v_accvgpr_write_b32 a38, 0\n v_accvgpr_write_b32 a39, 0\n"
+      "v_accvgpr_write_b32 a40, 0\n v_accvgpr_write_b32 a41, 0\n v_accvgpr_write_b32 a42, 0\n v_accvgpr_write_b32 a43, 0\n"
+      "v_accvgpr_write_b32 a44, 0\n v_accvgpr_write_b32 a45, 0\n v_accvgpr_write_b32 a46, 0\n v_accvgpr_write_b32 a47, 0\n"
+      "v_accvgpr_write_b32 a48, 0\n v_accvgpr_write_b32 a49, 0\n v_accvgpr_write_b32 a50, 0\n v_accvgpr_write_b32 a51, 0\n"
+      "v_accvgpr_write_b32 a52, 0\n v_accvgpr_write_b32 a53, 0\n v_accvgpr_write_b32 a54, 0\n v_accvgpr_write_b32 a55, 0\n"
+      "v_accvgpr_write_b32 a56, 0\n v_accvgpr_write_b32 a57, 0\n v_accvgpr_write_b32 a58, 0\n v_accvgpr_write_b32 a59, 0\n"
+      "v_accvgpr_write_b32 a60, 0\n v_accvgpr_write_b32 a61, 0\n v_accvgpr_write_b32 a62, 0\n v_accvgpr_write_b32 a63, 0\n"
+      "v_accvgpr_write_b32 a64, 0\n v_accvgpr_write_b32 a65, 0\n v_accvgpr_write_b32 a66, 0\n v_accvgpr_write_b32 a67, 0\n"
+      ::: H3P_CLOBBERS);
+  __syncthreads();
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  for (int i = 0; i < iters; i++) {
+    if constexpr (kMix == 0) {
+      asm volatile(H3P_MF0 H3P_MF1 H3P_MF2 H3P_MF3 ::: H3P_CLOBBERS);
+    } else if constexpr (kMix == 1) {
+      asm volatile(H3P_MF0 H3P_SM0 H3P_MF1 H3P_SM1 H3P_MF2 H3P_SM2 H3P_MF3 H3P_SM3 ::: H3P_CLOBBERS);
+    } else if constexpr (kMix == 2) {
+      asm volatile(H3P_MF0 H3P_SM0 H3P_DOT(28) H3P_MF1 H3P_SM1 H3P_MF2 H3P_SM2 H3P_DOT(29)
+                   H3P_MF3 H3P_SM3 ::: H3P_CLOBBERS);
+    } else if constexpr (kMix == 3) {
+      asm volatile(H3P_MF0 H3P_SM0 H3P_ADD(30) H3P_MF1 H3P_SM1 H3P_ADD(31) H3P_MF2 H3P_SM2
+                   H3P_ADD(32) H3P_MF3 H3P_SM3 H3P_ADD(33) ::: H3P_CLOBBERS);
+    } else {
+      asm volatile(H3P_MF0 H3P_SM0 H3P_M4 H3P_MF1 H3P_SM1 H3P_MF2 H3P_SM2 H3P_MF3
+                   H3P_SM3 ::: H3P_CLOBBERS);
+    }
+  }
+  // Let the last MFMAs and dots drain before the clock is read again.
+  asm volatile("s_nop 15\n s_nop 15\n s_nop 15\n s_nop 15" ::: "memory");
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  if ((threadIdx.x & 63) == 0) cycles[blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)] = t1 - t0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -332,6 +434,29 @@ int h3probe_relayout(int32_t variant, const void* in, void* out, int32_t rows, i
     case 8: relayout_stream<16, 5, 512, 0, 1><<<rows_pad / 16, 512, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
     case 9: relayout_stream<32, 5, 512, 0, 0><<<rows_pad / 32, 512, 0, s>>>(i4, o4, rows, rows_pad, heads); break;
     default: return -1;
+  }
+  return launch_status();
+}
+
+// Operand buffer size in bytes of h3probe_issue for `blocks` workgroups.
+int64_t h3probe_issue_operand_bytes(int32_t blocks) { return (int64_t)blocks * kThreads * 64; }
+
+// Issue mix `mix` (0..4, see issue_mix) on `blocks` workgroups of 8 waves (one
+// per CU), `iters` iterations; `ops` holds h3probe_issue_operand_bytes(blocks)
+// random bytes, `cycles` receives blocks * 8 shader-clock counts, one per
+// wave. Returns 0, -1 on a bad argument, -2 on a launch failure.
+int h3probe_issue(int32_t mix, const void* ops, int32_t blocks, int32_t iters, void* cycles,
+                  void* stream) {
+  if (mix < 0 || mix > 4 || !ops || !cycles || blocks <= 0 || iters <= 0) return -1;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const u32x4* o = static_cast<const u32x4*>(ops);
+  unsigned long long* c = static_cast<unsigned long long*>(cycles);
+  switch (mix) {
+    case 0: issue_mix<0><<<blocks, kThreads, 0, s>>>(o, iters, c); break;
+    case 1: issue_mix<1><<<blocks, kThreads, 0, s>>>(o, iters, c); break;
+    case 2: issue_mix<2><<<blocks, kThreads, 0, s>>>(o, iters, c); break;
+    case 3: issue_mix<3><<<blocks, kThreads, 0, s>>>(o, iters, c); break;
+    default: issue_mix<4><<<blocks, kThreads, 0, s>>>(o, iters, c); break;
   }
   return launch_status();
 }
