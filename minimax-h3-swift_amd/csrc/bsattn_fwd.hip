@@ -38,7 +38,10 @@
 // weight times a zeroed V row is NaN.)
 // The rescale is lazy: m is only raised when a tile's max exceeds it by more
 // than 2^8, which keeps every exponentiated score <= 256 and changes nothing
-// in exact arithmetic (numerator and denominator share m). l sums the fp32
+// in exact arithmetic (numerator and denominator share m). After a row's
+// first tile the loop takes the row max only when it may matter: it weighs
+// a tile at the current m first, and reruns the full step (max, raise,
+// alpha, weights) when the weights of a lane sum past 2^8 or to NaN. l sums the fp32
 // weights, as the reference's recurrence does; O accumulates their bf16
 // roundings, the P operand of the P V product. The output is O / max(l, 1e-30).
 #include <cmath>

@@ -33,7 +33,8 @@ Registers (physical, fixed here):
   v[122:126]  softmax temporaries
   s[64:88]    resources, column indices, raise mask (clobbered)
 With AGPRs in use the compiler gives a wave at most 128 VGPRs and 128 AGPRs
-when two waves share a SIMD; this map uses 127 and 123.
+when two waves share a SIMD; this map uses 127 and 123
+(the compiler needs one VGPR of its own beside the block).
 
 Run `python3 gen_tile_loop.py` in this directory after editing; the generated
 file is committed, and tests/test_tile_loop_gen.py checks it is current.
@@ -98,6 +99,7 @@ VA0 = 106       # V^T operand address (p, db): v[106 + 4p + db]
 DK0 = 114       # K load lane offsets: v[114 + i], i < LOADS
 DV0 = DK0 + LOADS  # V load lane offsets
 MX, SW, AL, LA, LB = 122, 123, 124, 125, 126
+T4 = (MX, SW, AL, LB)    # temporaries of the fast softmax
 N_VGPR = 127
 KEYOFF = 120    # a120: kh*64 + 4hh            (input)
 LANE16 = 121    # a121: 16 * lane              (input)
@@ -125,6 +127,7 @@ def fbits(x: float) -> str:
 NEG_INF = "0xff800000"
 M_INIT = fbits(-3.0e38)
 SLACK = fbits(8.0)
+SUM_LIMIT = fbits(256.0)   # 2^SLACK
 
 
 # ------------------------------------------------------------- MFMA streams
@@ -226,6 +229,42 @@ def softmax_ops(sb, pb):
     ops.append(f"v_add_f32 v{L}, v{L}, v{LA}")
     return ops
 
+
+
+def softmax_fast_ops(sb, pb):
+    """The online softmax of S(sb) into P(pb) for a tile that does not move m
+    (almost every tile after a row's first): weights 2^(s*c - m) with the
+    current m, packed to P and summed in fp32 into LA (one chain), with the
+    scores left in place. No row max: the raise mask marks the lanes whose
+    weights sum to more than 2^8, or to NaN. Every tile softmax_ops would
+    raise m for has a weight above 2^8 and is marked; for a marked tile the
+    block end reruns softmax_ops on the kept scores, so m, P and l are what
+    softmax_ops gives. Unmarked, P is bit for bit the same (alpha is 1
+    there) and l differs only in the order of the sum; l += LA is left to
+    the block end. The row max and the alpha update are the ~30 VALU
+    instructions a tile saves: past ~4 VALU instructions per MFMA the two
+    waves of a SIMD no longer hide their VALU work under the matrix cores."""
+    x = [s_reg(sb, i) for i in range(32)]
+    t = T4
+    ops = []
+    for b in range(8):
+        for k in range(4):
+            ops.append(f"v_fma_f32 v{t[k]}, v{x[4 * b + k]}, %[c], -v{M}")
+        for k in range(4):
+            ops.append(f"v_exp_f32 v{t[k]}, v{t[k]}")
+        for pair in range(2):
+            i0 = 4 * b + 2 * pair
+            kb, r = i0 // 16, i0 % 16
+            dst = p_reg(pb, 2 * kb + (r >> 3), (r & 7) >> 1)
+            ops.append(f"v_cvt_pk_bf16_f32 v{dst}, v{t[2 * pair]}, v{t[2 * pair + 1]}")
+            if b == 0 and pair == 0:   # the chain starts from the tile's first pair
+                ops.append(f"v_add_f32 v{LA}, v{t[0]}, v{t[1]}")
+            else:
+                ops.append(f"v_add_f32 v{LA}, v{LA}, v{t[2 * pair]}")
+                ops.append(f"v_add_f32 v{LA}, v{LA}, v{t[2 * pair + 1]}")
+    ops.append(f"s_mov_b32 {ST0}, {SUM_LIMIT}")
+    ops.append(f"v_cmp_nge_f32 {RAISE}, {ST0}, v{LA}")
+    return ops
 
 def mask_ops(sb, pb):
     """Scores of keys >= seq_len set to -inf (ragged last tile). Uses three
@@ -343,11 +382,17 @@ def schedule(em, ops, valu, dmas, lookahead=LOOKAHEAD, pre=None, dma_at=None):
 
 
 # ------------------------------------------------------------------ blocks
-def rescale_code(em, label, sb):
-    """Out of line: O *= alpha, after the PV MFMAs drain. Temporaries are
-    the scores S(sb), consumed by this point."""
+def fixup_code(em, label, sb, pb):
+    """Out of line, for a FULL/LAST block whose fast softmax marked lanes:
+    softmax_ops reruns on the kept scores S(sb) -- row max, lazy raise,
+    alpha, the weights into P(pb) again, l = alpha l + their sum -- and if m
+    moved in any lane, O *= alpha once the P V MFMAs have drained. The
+    rescale's temporaries are the scores, consumed by then."""
+    em.emit(f"{label}_fixup:")
+    em.emit(*softmax_ops(sb, pb))
+    em.emit(f"s_cmp_lg_u64 {RAISE}, 0", f"s_cbranch_scc0 {label}_rescaled")
     t = [s_reg(sb, i) for i in range(4)]
-    em.emit(f"{label}_rescale:", "s_nop 15", "s_nop 15", "s_nop 15", "s_nop 15")
+    em.emit("s_nop 15", "s_nop 15", "s_nop 15", "s_nop 15")
     for db in range(4):
         for r0 in range(0, 16, 4):
             for r in range(4):
@@ -373,11 +418,17 @@ def column_load():
 
 
 def block_end(em, kind, p, label, sb):
-    """Rescale (FULL/LAST), waits (which also collect the column load of
-    FIRST/FULL blocks), ragged V zeroing (LAST/ONLY), barrier, column shift."""
+    """The fast softmax's outcome (FULL/LAST: marked lanes branch to the
+    fixup, otherwise l += the tile's sum), waits (which also collect the
+    column load of FIRST/FULL blocks), ragged V zeroing (LAST/ONLY),
+    barrier, column shift."""
     if kind in ("FULL", "LAST"):
-        em.emit(f"s_cmp_lg_u64 {RAISE}, 0",
-                f"s_cbranch_scc1 {label}_rescale",
+        # s_nop: the raise mask may have been written by the block's last VALU
+        # instruction.
+        em.emit("s_nop 4",
+                f"s_cmp_lg_u64 {RAISE}, 0",
+                f"s_cbranch_scc1 {label}_fixup",
+                f"v_add_f32 v{L}, v{L}, v{LA}",
                 f"{label}_rescaled:")
     em.emit("s_waitcnt vmcnt(0) lgkmcnt(0)")
     if kind in ("LAST", "ONLY"):
@@ -458,7 +509,7 @@ def gen_block(em, kind, p, label, out_of_line):
             dmas.append(vd[i])
     sops = s_ops(sn, sn) if has_s else []
     pops = pv_ops(pp, pp) if has_pv else []
-    valu = softmax_ops(sc, pn)
+    valu = softmax_fast_ops(sc, pn) if has_pv else softmax_ops(sc, pn)
     ops = sops + pops
     dma_at = dma_quota(len(ops), len(dmas)) if ops else None
     if kind in ("LAST", "ONLY"):
@@ -473,7 +524,7 @@ def gen_block(em, kind, p, label, out_of_line):
     block_end(em, kind, p, label, sc)
     if has_pv:
         sub = Emitter()
-        rescale_code(sub, label, sc)
+        fixup_code(sub, label, sc, pn)
         out_of_line.extend(sub.lines)
 
 

@@ -22,6 +22,8 @@ import importlib.util
 import os
 import re
 
+import numpy as np
+
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -274,3 +276,138 @@ def test_column_load_early_and_collected(gen, lines):
         between = lines[i + 1:j]
         assert sum(ln.startswith("v_mfma") for ln in between) >= 8, lines[i]
         assert not any(gen.SCOL in ln for ln in between), lines[i]
+
+
+class _Lanes:
+    """A 64-lane model of the VALU/SALU subset the softmax code uses, in fp32
+    (v_exp_f32 as numpy's exp2: the same function on both sides of each
+    comparison below, so equalities are exact)."""
+
+    def __init__(self, c):
+        self.v = np.zeros((128, 64), dtype=np.float32)
+        self.s = {}
+        self.c = np.float32(c)
+
+    def src(self, tok):
+        tok = tok.strip()
+        neg = tok.startswith("-")
+        tok = tok.lstrip("-")
+        if tok == "%[c]":
+            val = np.full(64, self.c, dtype=np.float32)
+        elif re.fullmatch(r"v\d+", tok):
+            val = self.v[int(tok[1:])].copy()
+        elif re.fullmatch(r"s\d+", tok):
+            val = np.full(64, np.uint32(self.s[tok]).view(np.float32), dtype=np.float32)
+        elif tok.startswith("0x"):
+            val = np.full(64, np.uint32(int(tok, 16)).view(np.float32), dtype=np.float32)
+        else:
+            val = np.full(64, np.float32(float(tok)), dtype=np.float32)
+        return -val if neg else val
+
+    def run(self, lines):
+        for ln in lines:
+            op, parts = _split(ln)
+            d = parts[0]
+            if op in ("s_nop",):
+                continue
+            if op == "s_mov_b32":
+                self.s[d] = int(parts[1], 16) if parts[1].startswith("0x") else int(parts[1])
+                continue
+            a = [self.src(p) for p in parts[1:] if not p.startswith("s[")]
+            with np.errstate(over="ignore", invalid="ignore"):
+                if op == "v_fma_f32":
+                    r = (a[0].astype(np.float64) * a[1] + a[2]).astype(np.float32)
+                elif op == "v_exp_f32":
+                    r = np.exp2(a[0])
+                elif op == "v_add_f32":
+                    r = a[0] + a[1]
+                elif op == "v_sub_f32":
+                    r = a[0] - a[1]
+                elif op == "v_mul_f32":
+                    r = a[0] * a[1]
+                elif op == "v_max_f32":
+                    r = np.maximum(a[0], a[1])
+                elif op == "v_max3_f32":
+                    r = np.maximum(np.maximum(a[0], a[1]), a[2])
+                elif op == "v_mov_b32":
+                    r = a[0]
+                elif op == "v_cvt_pk_bf16_f32":
+                    def bf(x):
+                        u = x.view(np.uint32).astype(np.uint64)
+                        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+                    r = (bf(a[0]) | (bf(a[1]) << 16)).view(np.float32)
+                elif op == "v_permlane32_swap_b32":
+                    i, j = int(d[1:]), int(parts[1][1:])
+                    hi = self.v[i, 32:].copy()
+                    self.v[i, 32:] = self.v[j, :32]
+                    self.v[j, :32] = hi
+                    continue
+                elif op in ("v_cmp_gt_f32", "v_cmp_nge_f32"):
+                    m = a[0] > a[1] if op == "v_cmp_gt_f32" else ~(a[0] >= a[1])
+                    self.s[d] = m
+                    continue
+                elif op == "v_cndmask_b32":
+                    r = np.where(self.s[parts[3]], a[1], a[0])
+                else:
+                    raise AssertionError(f"model has no {op}")
+            self.v[int(d[1:])] = r
+
+
+def _softmax_state(gen, sb, seed, lift):
+    rng = np.random.default_rng(seed)
+    lanes = _Lanes(c=0.1275)
+    scores = rng.normal(0.0, 8.0, (32, 64)).astype(np.float32)
+    # m: the running max of earlier tiles, at or above this tile's max, except
+    # in the lanes listed in `lift`, whose scores then exceed m by > 2^8.
+    tmax = np.maximum(scores.reshape(32, 2, 32).max(axis=(0, 1)), -1e30)
+    m = (np.tile(tmax, 2) * lanes.c + rng.uniform(0.0, 3.0, 64)).astype(np.float32)
+    for lane in lift:
+        scores[rng.integers(32), lane] = (m[lane] + 9.0 + rng.uniform(0, 4)) / lanes.c
+    for i in range(32):
+        lanes.v[gen.s_reg(sb, i)] = scores[i]
+    lanes.v[gen.M] = m
+    lanes.v[gen.L] = rng.uniform(1.0, 50.0, 64).astype(np.float32)
+    return lanes
+
+
+def _p_bits(lanes, gen, pb):
+    return np.stack([lanes.v[gen.p_reg(pb, kc, e)].view(np.uint32)
+                     for kc in range(4) for e in range(4)])
+
+
+@pytest.mark.parametrize("sb, pb", [(0, 0), (1, 1), (0, 1), (1, 0)])
+def test_fast_softmax_matches_full_softmax(gen, sb, pb):
+    """The block end reruns the full recurrence for the whole wave when any
+    lane is marked. So: every query (lanes i and i ^ 32) the full recurrence
+    raises m for has a marked lane; and with no lane marked the fast path's
+    weights are the full recurrence's bit for bit, its l equal to rounding,
+    and the scores are still in place."""
+    for seed, lift in ((1, ()), (4, ()), (2, (3, 40)), (3, tuple(range(0, 64, 5)))):
+        full = _softmax_state(gen, sb, seed, lift)
+        fast = _softmax_state(gen, sb, seed, lift)
+        full.run(gen.softmax_ops(sb, pb))
+        fast.run(gen.softmax_fast_ops(sb, pb))
+        raised = full.s[gen.RAISE]
+        marked = fast.s[gen.RAISE]
+        pair_marked = marked | np.roll(marked, 32)
+        assert np.all(pair_marked[raised]), (seed, np.nonzero(raised & ~pair_marked))
+        assert raised.any() == bool(lift) and marked.any() == bool(lift)
+        if lift:
+            continue
+        assert np.array_equal(_p_bits(full, gen, pb), _p_bits(fast, gen, pb))
+        l_fast = fast.v[gen.L] + fast.v[gen.LA]          # the block end's l += LA
+        np.testing.assert_allclose(l_fast, full.v[gen.L], rtol=1e-6)
+        kept = _softmax_state(gen, sb, seed, lift)
+        for i in range(32):
+            assert np.array_equal(fast.v[gen.s_reg(sb, i)], kept.v[gen.s_reg(sb, i)])
+
+
+def test_fast_softmax_test_catches_a_dropped_weight(gen):
+    """The comparison above fails when the fast path leaves a weight out of l."""
+    ops = gen.softmax_fast_ops(0, 0)
+    i = next(k for k, ln in enumerate(ops) if ln.startswith(f"v_add_f32 v{gen.LA}, v{gen.LA}, v"))
+    full = _softmax_state(gen, 0, 1, ())
+    fast = _softmax_state(gen, 0, 1, ())
+    full.run(gen.softmax_ops(0, 0))
+    fast.run(ops[:i] + ops[i + 1:])
+    assert not np.allclose(fast.v[gen.L] + fast.v[gen.LA], full.v[gen.L], rtol=1e-6)
