@@ -184,8 +184,10 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < kRowsPerWave / 4; i++) {
         const int row = kRowsPerWave * wave + 4 * i + (lane >> 4);
-        dk[i] = row * k_rs2 + (((lane & 15) ^ k_swz(row)) * 16);
-        dv[i] = row * v_rs2 + (((lane & 15) ^ v_swz(row)) * 16);
+        // Less 1024 i: the tile loop's loads add it back as their
+        // instruction offset, which also steps their LDS address.
+        dk[i] = row * k_rs2 + (((lane & 15) ^ k_swz(row)) * 16) - 1024 * i;
+        dv[i] = row * v_rs2 + (((lane & 15) ^ v_swz(row)) * 16) - 1024 * i;
       }
       const int keyoff = kh * 64 + 4 * hh, lane16 = 16 * lane;
       const int rowb = kRowsPerWave * wave + (lane >> 4);

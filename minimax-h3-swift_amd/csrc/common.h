@@ -55,8 +55,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 __device__ __forceinline__ float round_bf16(float f) {
   return __uint_as_float(f32_to_bf16_bits(f) << 16);
 }
+// Two floats to packed bf16 (lo in bits 0-15), round to nearest even: on gfx950
+// one v_cvt_pk_bf16_f32, the same rounding as f32_to_bf16_bits for finite
+// values (NaN stays NaN here; f32_to_bf16_bits can carry a NaN's low bits
+// into the sign).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 }  // namespace h3hip

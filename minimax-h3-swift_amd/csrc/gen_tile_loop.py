@@ -296,15 +296,17 @@ def rsrc_setup(which, col, base_lo, base_hi, rec, stride128):
 
 
 def dma_lines(which, slot):
-    """This wave's buffer loads of its rows of a K or V tile into the slot."""
+    """This wave's buffer loads of its rows of a K or V tile into the slot,
+    in order: one M0 for the tile, the loads' instruction offsets (which
+    apply to the LDS and to the global address alike) for their 1 KiB steps;
+    the lane offsets v[DK0/DV0 + i] are lowered by the same 1024 i."""
+    m0 = "%[m0k]" if which == "k" else "%[m0v]"
+    base = DK0 if which == "k" else DV0
+    rs = KRS if which == "k" else VRS
     out = []
     for i in range(LOADS):
-        m0 = "%[m0k]" if which == "k" else "%[m0v]"
-        voff = (DK0 if which == "k" else DV0) + i
-        rs = KRS if which == "k" else VRS
-        imm = slot * KSLOT + 1024 * i
-        out.append([f"s_add_u32 m0, {m0}, {imm}", "s_nop 0",
-                    f"buffer_load_dwordx4 v{voff}, {rs}, 0 offen lds"])
+        ld = f"buffer_load_dwordx4 v{base + i}, {rs}, 0 offen offset:{1024 * i} lds"
+        out.append(([f"s_add_u32 m0, {m0}, {slot * KSLOT}", "s_nop 0"] if i == 0 else []) + [ld])
     return out
 
 
@@ -501,12 +503,7 @@ def gen_block(em, kind, p, label, out_of_line):
     if has_s:
         pre += column_load()
     vd = dma_lines("v", p)
-    dmas = []
-    for i in range(max(len(kd), len(vd))):
-        if i < len(kd):
-            dmas.append(kd[i])
-        if i < len(vd):
-            dmas.append(vd[i])
+    dmas = kd + vd     # each tile's loads together: they share its M0
     sops = s_ops(sn, sn) if has_s else []
     pops = pv_ops(pp, pp) if has_pv else []
     valu = softmax_fast_ops(sc, pn) if has_pv else softmax_ops(sc, pn)
