@@ -81,6 +81,7 @@ struct AttnArgs {
   const int32_t* __restrict__ col_idx;
   const int32_t* __restrict__ work_ptr;  // [groups + 1]
   const int32_t* __restrict__ work;
+  const int32_t* __restrict__ unit_desc;  // [units][kUnitDescInts], in work order
   int64_t q_hs, k_hs, v_hs, o_hs;  // head strides (elements)
   int32_t q_rs, k_rs, v_rs, o_rs;  // row strides (elements)
   int32_t seq_len, out_rows;
@@ -100,6 +101,12 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 __host__ __device__ __forceinline__ int k_swz(int r) { return r & 15; }
 __host__ __device__ __forceinline__ int v_swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
 
+// Workgroup barrier ordering this wave's LDS accesses only (not its
+// outstanding global loads and stores, which __syncthreads would also wait for).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -109,8 +116,17 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // K-swizzled, into K slot 0 and the Q slot. Buffer resources bound the rows
 // at seq_len, so no row past it is fetched; query rows past it only feed
 // output rows that are stored as zeros.
-__device__ __forceinline__ void load_unit_start(const AttnArgs& a, uint16_t* lds, int32_t unit,
+// Unit iu's descriptor (plan.h: unit, col_idx index, n, c0, c1, c2, ragged),
+// through the scalar cache.
+__device__ __forceinline__ const __attribute__((address_space(4))) int32_t* unit_desc(
+    const AttnArgs& a, int iu) {
+  return (const __attribute__((address_space(4))) int32_t*)(a.unit_desc) + kUnitDescInts * iu;
+}
+
+__device__ __forceinline__ void load_unit_start(const AttnArgs& a, uint16_t* lds, int iu,
                                                 int wave, int lane) {
+  const auto* d = unit_desc(a, iu);
+  const int32_t unit = d[0];
   const int head = unit >> 16, qt = unit & 0xffff;
   const int dma_row = kRowsPerWave * wave + (lane >> 4);
   auto tile = [&](const uint16_t* base, int rs2, int row0, uint16_t* slot)
@@ -126,12 +142,7 @@ __device__ __forceinline__ void load_unit_start(const AttnArgs& a, uint16_t* lds
     }
   };
   tile(a.q + head * a.q_hs, a.q_rs * 2, qt * kTile, lds + kQSlot / 2);
-  const int beg = a.row_ptr[qt];
-  if (a.row_ptr[qt + 1] > beg) {
-    const int32_t first_col =
-        *((const __attribute__((address_space(4))) int32_t*)(a.col_idx) + beg);
-    tile(a.k + head * a.k_hs, a.k_rs * 2, first_col * kTile, lds + kKSlot0 / 2);
-  }
+  if (d[2] > 0) tile(a.k + head * a.k_hs, a.k_rs * 2, d[3] * kTile, lds + kKSlot0 / 2);
 }
 
 __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
@@ -143,7 +154,32 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
   const uint32_t base = lds_addr(lds);
 
   const int u_beg = a.work_ptr[blockIdx.x], u_end = a.work_ptr[blockIdx.x + 1];
-  if (u_beg < u_end) load_unit_start(a, lds, a.work[u_beg], wave, threadIdx.x & 63);
+  if (u_beg < u_end) load_unit_start(a, lds, u_beg, wave, threadIdx.x & 63);
+  // Lane address offsets of the tile loop (bytes), the same for every unit:
+  // computed once; the tile loop takes them as inputs and leaves them intact.
+  const int lane0 = threadIdx.x & 63, li0 = lane0 & 31, hh0 = lane0 >> 5;
+  int ka[8], va[8], dk[kRowsPerWave / 4], dv[kRowsPerWave / 4];
+#pragma unroll
+  for (int s = 0; s < 8; s++)
+    ka[s] = base + kKSlot0 + 2 * ((kh * 64 + li0) * kD + (((2 * s + hh0) ^ k_swz(li0)) * 8));
+  const int g = lane0 >> 4, mm = lane0 & 15;
+#pragma unroll
+  for (int p = 0; p < 2; p++)
+#pragma unroll
+    for (int db = 0; db < 4; db++) {
+      const int row = kh * 64 + 8 * p + 4 * (g >> 1) + (mm >> 2);
+      const int chunk = 4 * db + 2 * (g & 1) + ((mm & 3) >> 1);
+      va[4 * p + db] =
+          base + kVSlot0 + 2 * (row * kD + ((chunk ^ v_swz(row)) * 8) + 4 * (mm & 1));
+    }
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave / 4; i++) {
+    const int row = kRowsPerWave * wave + 4 * i + (lane0 >> 4);
+    // Less 1024 i: the tile loop's loads add it back as their
+    // instruction offset, which also steps their LDS address.
+    dk[i] = row * k_rs2 + (((lane0 & 15) ^ k_swz(row)) * 16) - 1024 * i;
+    dv[i] = row * v_rs2 + (((lane0 & 15) ^ v_swz(row)) * 16) - 1024 * i;
+  }
   for (int iu = u_beg; iu < u_end; iu++) {
     // Lane-derived values are rebuilt for each unit from an opaque copy of the
     // thread index: hoisted out of the unit loop they would stay live across
@@ -151,12 +187,11 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
     int tid;
     asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(threadIdx.x));
     const int lane = tid & 63, li = lane & 31, hh = lane >> 5;
-    const int32_t unit = a.work[iu];
+    const auto* desc = unit_desc(a, iu);
+    const int32_t unit = desc[0];
     const int head = unit >> 16, qt = unit & 0xffff;
     const int q0 = qt * kTile + qg * 32;
-    const int beg = a.row_ptr[qt], n = a.row_ptr[qt + 1] - beg;
-    const __attribute__((address_space(4))) int32_t* cols =
-        (const __attribute__((address_space(4))) int32_t*)(a.col_idx) + beg;
+    const int beg = desc[1], n = desc[2];
 
     // The unit's K(0) and Q have landed (each wave waits for its own loads),
     // and the previous unit's merge buffers have been read.
@@ -166,37 +201,14 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
     f32x32 o01, o23;  // O(0), O(1) and O(2), O(3): 16 accumulators each
     float m, l;
     if (n > 0) {
-      // Lane address offsets for the tile loop (bytes).
-      int ka[8], va[8], dk[kRowsPerWave / 4], dv[kRowsPerWave / 4];
-#pragma unroll
-      for (int s = 0; s < 8; s++)
-        ka[s] = base + kKSlot0 + 2 * ((kh * 64 + li) * kD + (((2 * s + hh) ^ k_swz(li)) * 8));
-      const int g = lane >> 4, mm = lane & 15;
-#pragma unroll
-      for (int p = 0; p < 2; p++)
-#pragma unroll
-        for (int db = 0; db < 4; db++) {
-          const int row = kh * 64 + 8 * p + 4 * (g >> 1) + (mm >> 2);
-          const int chunk = 4 * db + 2 * (g & 1) + ((mm & 3) >> 1);
-          va[4 * p + db] =
-              base + kVSlot0 + 2 * (row * kD + ((chunk ^ v_swz(row)) * 8) + 4 * (mm & 1));
-        }
-#pragma unroll
-      for (int i = 0; i < kRowsPerWave / 4; i++) {
-        const int row = kRowsPerWave * wave + 4 * i + (lane >> 4);
-        // Less 1024 i: the tile loop's loads add it back as their
-        // instruction offset, which also steps their LDS address.
-        dk[i] = row * k_rs2 + (((lane & 15) ^ k_swz(row)) * 16) - 1024 * i;
-        dv[i] = row * v_rs2 + (((lane & 15) ^ v_swz(row)) * 16) - 1024 * i;
-      }
+
       const int keyoff = kh * 64 + 4 * hh, lane16 = 16 * lane;
       const int rowb = kRowsPerWave * wave + (lane >> 4);
 
       // Scalar operands of the tile loop, made wave-uniform explicitly so they
       // are SGPRs.
       auto u = [](uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); };
-      const uint32_t c0 = u(cols[0]), c1 = u(cols[n > 1 ? 1 : 0]), c2 = u(cols[n > 2 ? 2 : n - 1]);
-      const uint32_t ragged = u((cols[n - 1] * kTile + kTile > a.seq_len) ? 1u : 0u);
+      const uint32_t c0 = u(desc[3]), c1 = u(desc[4]), c2 = u(desc[5]), ragged = u(desc[6]);
       const uint64_t colp = (uint64_t)(uintptr_t)(a.col_idx + beg);
       const uint64_t kbp = (uint64_t)(uintptr_t)(a.k + head * a.k_hs);
       const uint64_t vbp = (uint64_t)(uintptr_t)(a.v + head * a.v_hs);
@@ -238,8 +250,11 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
     const int lane2 = tid & 63, li2 = lane2 & 31, hh2 = lane2 >> 5;
     // The next unit's K(0) and Q go into K slot 0 and the Q slot, which no
     // wave reads once its tile loop has passed the last tile's barrier.
-    if (iu + 1 < u_end) load_unit_start(a, lds, a.work[iu + 1], wave, lane2);
-    __syncthreads();  // every wave's last V reads are done: the V slots are free
+    if (iu + 1 < u_end) load_unit_start(a, lds, iu + 1, wave, lane2);
+    // Every wave's last V reads are done: the V slots are free. An LDS-only
+    // barrier: __syncthreads would also wait for the loads just issued, whose
+    // HBM latency the merge is there to cover (the next unit waits for them).
+    lds_barrier();
 
     // Merge of the two key halves (exact: both rescaled to the larger m).
     // Wave (qg, kh) finalises channel blocks 2kh, 2kh+1 of its 32 queries and
@@ -266,7 +281,7 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
         }
       xml[wave * 128 + lane2] = m;
       xml[wave * 128 + 64 + lane2] = lt;
-      __syncthreads();
+      lds_barrier();
       const int pw = wave ^ 4;
       const float* theirs = xo + pw * 2048;
       const float mp = xml[pw * 128 + lane2], ltp = xml[pw * 128 + 64 + lane2];
@@ -323,6 +338,7 @@ static int launch_bsattn(h3hip_plan p, const View& q, const View& k, const View&
                 p->d_col_idx,
                 p->d_work_ptr,
                 p->d_work,
+                p->d_unit_desc,
                 q.head_stride,
                 k.head_stride,
                 v.head_stride,

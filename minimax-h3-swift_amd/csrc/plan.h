@@ -28,7 +28,17 @@ struct h3hip_plan_s {
   int32_t* d_col_idx = nullptr;
   int32_t* d_work_ptr = nullptr;
   int32_t* d_work = nullptr;
+  // One descriptor per unit, in work order, kUnitDescInts int32 each: what
+  // the attention kernel needs at a unit's start, in one scalar load instead
+  // of a chain of dependent ones (unit -> row_ptr -> col_idx).
+  std::vector<int32_t> unit_desc;
+  int32_t* d_unit_desc = nullptr;
 };
+
+// Unit descriptor layout: unit (head << 16 | q_tile), first index of the row
+// in col_idx, tile count n, columns c0, c1, c2 (the first three, repeating the
+// last when n < 3), ragged (1 when the last tile runs past seq_len), unused.
+constexpr int kUnitDescInts = 8;
 
 namespace h3hip {
 

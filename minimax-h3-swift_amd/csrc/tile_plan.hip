@@ -508,16 +508,37 @@ int h3hip_plan_create(const h3hip_mask_rule* rule, int32_t heads, const h3hip_po
   p->groups = std::max(8, cus / 8 * 8);
   rc = build_schedule(p->row_ptr, heads, p->groups, p->work_ptr, p->work);
   if (rc) return fail(rc);
+  p->unit_desc.assign(p->work.size() * kUnitDescInts, 0);
+  for (size_t u = 0; u < p->work.size(); u++) {
+    const int32_t unit = p->work[u], qt = unit & 0xffff;
+    const int32_t beg = p->row_ptr[qt], n = p->row_ptr[qt + 1] - beg;
+    int32_t* d = &p->unit_desc[kUnitDescInts * u];
+    d[0] = unit;
+    d[1] = beg;
+    d[2] = n;
+    if (n > 0) {
+      const int32_t* c = &p->col_idx[beg];
+      d[3] = c[0];
+      d[4] = c[n > 1 ? 1 : 0];
+      d[5] = c[n > 2 ? 2 : n - 1];
+      d[6] = (int64_t)c[n - 1] * 128 + 128 > p->seq_len ? 1 : 0;
+    }
+  }
+  const size_t desc_bytes = sizeof(int32_t) * std::max<size_t>(p->unit_desc.size(), 1);
   if (hipMalloc(&p->d_work_ptr, sizeof(int32_t) * p->work_ptr.size()) != hipSuccess ||
-      hipMalloc(&p->d_work, sizeof(int32_t) * std::max<size_t>(p->work.size(), 1)) != hipSuccess) {
+      hipMalloc(&p->d_work, sizeof(int32_t) * std::max<size_t>(p->work.size(), 1)) != hipSuccess ||
+      hipMalloc(&p->d_unit_desc, desc_bytes) != hipSuccess) {
     set_error("device allocation for the work list failed");
     return fail(H3HIP_ENOMEM);
   }
   if (hipMemcpyAsync(p->d_work_ptr, p->work_ptr.data(), sizeof(int32_t) * p->work_ptr.size(),
                      hipMemcpyHostToDevice, s) != hipSuccess ||
       (!p->work.empty() &&
-       hipMemcpyAsync(p->d_work, p->work.data(), sizeof(int32_t) * p->work.size(),
-                      hipMemcpyHostToDevice, s) != hipSuccess) ||
+       (hipMemcpyAsync(p->d_work, p->work.data(), sizeof(int32_t) * p->work.size(),
+                       hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(p->d_unit_desc, p->unit_desc.data(),
+                       sizeof(int32_t) * p->unit_desc.size(), hipMemcpyHostToDevice,
+                       s) != hipSuccess)) ||
       hipStreamSynchronize(s) != hipSuccess) {
     set_error("uploading the work list failed");
     return fail(H3HIP_EHIP);
@@ -532,6 +553,7 @@ int h3hip_plan_destroy(h3hip_plan p) {
   if (p->d_col_idx) (void)hipFree(p->d_col_idx);
   if (p->d_work) (void)hipFree(p->d_work);
   if (p->d_work_ptr) (void)hipFree(p->d_work_ptr);
+  if (p->d_unit_desc) (void)hipFree(p->d_unit_desc);
   delete p;
   return H3HIP_OK;
 }
