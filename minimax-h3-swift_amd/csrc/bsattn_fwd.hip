@@ -180,6 +180,8 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
     dk[i] = row * k_rs2 + (((lane0 & 15) ^ k_swz(row)) * 16) - 1024 * i;
     dv[i] = row * v_rs2 + (((lane0 & 15) ^ v_swz(row)) * 16) - 1024 * i;
   }
+  // The first unit's K(0) and Q have landed (later units wait in the merge).
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   for (int iu = u_beg; iu < u_end; iu++) {
     // Lane-derived values are rebuilt for each unit from an opaque copy of the
     // thread index: hoisted out of the unit loop they would stay live across
@@ -193,10 +195,11 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
     const int q0 = qt * kTile + qg * 32;
     const int beg = desc[1], n = desc[2];
 
-    // The unit's K(0) and Q have landed (each wave waits for its own loads),
-    // and the previous unit's merge buffers have been read.
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __syncthreads();
+    // The unit's K(0) and Q have landed (each wave waited for its own loads
+    // before its output stores) and the previous unit's merge buffers have
+    // been read. The output stores stay in flight: loads return in order, so
+    // the tile loop's counted waits only grow stronger for them.
+    lds_barrier();
 
     f32x32 o01, o23;  // O(0), O(1) and O(2), O(3): 16 accumulators each
     float m, l;
@@ -293,6 +296,9 @@ __global__ __launch_bounds__(kThreads, 1) void bsattn_fwd_kernel(AttnArgs a) {
       // 32db + 8gg + 4hh + [0, 4) in registers 16db + 4gg .. +3.
       const int qi = q0 + li2;
       const bool valid = qi < a.seq_len;
+      // This wave's loads of the next unit are done before its output
+      // stores are issued, so that the next unit waits for no store.
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
       if (qi < a.out_rows) {
         uint16_t* orow = a.out + head * a.o_hs + (int64_t)qi * a.o_rs;
 #pragma unroll
